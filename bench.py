@@ -1,0 +1,280 @@
+#!/usr/bin/env python3
+"""Benchmark of the forward-attention hot path on one MI355X.
+
+Headline workload: bf16 causal prefill, B=4, H=32, S=8192,
+D=128, through the drop-in ``fastest_flash_attn_forward``. A step is one forward over
+that batch with q/k/v already resident in HBM. Second workload in the same line:
+paged GQA decode (BASELINE cfg4: B=64, 32 q heads / 8 kv heads, D=128, page 16,
+context lengths U[512, 32768], random page permutation).
+
+Algorithmic work: prefill FLOPs = 4 * B * H * D * N_valid, N_valid = exact number of
+unmasked (q, k) pairs; decode bytes = K/V bytes of exactly context_len tokens + q + o +
+lse + block tables + context lengths (split-K workspace traffic not counted).
+
+Timing: HIP events recorded on the stream the kernels launch on (torch's current
+stream) around exactly --steps steps, after --warmup untimed steps, bracketed by
+torch.cuda.synchronize(). The CPU baseline is the oracle restatement of the reference
+CPU path (oracle/reference_forward.py) on a bounded row sample of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CU x 4096 flop/clk x 2.4 GHz)
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+
+PREFILL = {
+    "north_star": dict(B=4, Hq=32, Hkv=32, S=8192, D=128, causal=True, window=None, softcap=None),
+    "cfg2": dict(B=4, Hq=32, Hkv=32, S=4096, D=128, causal=True, window=None, softcap=None),
+    "cfg3": dict(B=2, Hq=32, Hkv=8, S=8192, D=128, causal=True, window=4096, softcap=50.0),
+    "cfg5": dict(B=2, Hq=32, Hkv=32, S=4096, D=192, causal=True, window=None, softcap=None),
+}
+
+
+def n_valid_pairs(S_q: int, S_kv: int, causal: bool, window, q_offset: int = 0) -> int:
+    """Exact count of visible (q, k) pairs per (batch, head)."""
+    total = 0
+    for i in range(S_q):
+        row = q_offset + i
+        hi = min(S_kv - 1, row) if causal else S_kv - 1
+        lo = max(0, row - window + 1) if window else 0
+        total += max(0, hi - lo + 1)
+    return total
+
+
+def n_valid_pairs_fast(S: int, causal: bool, window) -> int:
+    if not causal and not window:
+        return S * S
+    if causal and not window:
+        return S * (S + 1) // 2
+    return n_valid_pairs(S, S, causal, window)
+
+
+def time_steps(fn, steps: int, warmup: int):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(stop) / steps, wall * 1e3 / steps
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        n = [p["num_threads"] for p in threadpool_info() if p.get("user_api") == "blas"]
+        return max(n) if n else 1
+    except Exception:  # pragma: no cover - informational only
+        return 1
+
+
+def cpu_baseline_prefill(cfg: dict, q, k, v, budget_s: float) -> dict:
+    """Oracle restatement of the reference CPU path on a row band of head (0, 0),
+    with the reference dispatcher's block size; rows are independent given q_offset."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import reference_forward as rf
+
+    S, D = cfg["S"], cfg["D"]
+    bs = rf.auto_select_block_size(S, S, D)
+    q0 = q[0, 0].float().cpu().numpy()[None, None]
+    k0 = k[0, 0].float().cpu().numpy()[None, None]
+    v0 = v[0, 0].float().cpu().numpy()[None, None]
+
+    def run(r0, r1):
+        kv_end = r1 if cfg["causal"] else S
+        kv_lo = max(0, r0 - cfg["window"] + 1) if cfg["window"] else 0
+        kv_lo = (kv_lo // bs) * bs  # keep the reference's KV tile grid
+        t = time.perf_counter()
+        rf.flash_attn_cpu_forward(q0[:, :, r0:r1], k0[:, :, kv_lo:kv_end], v0[:, :, kv_lo:kv_end],
+                                  scale=1 / math.sqrt(D), causal=cfg["causal"], block_q=bs,
+                                  block_kv=bs, softcap=cfg["softcap"],
+                                  sliding_window=cfg["window"], q_offset=r0 - kv_lo)
+        return time.perf_counter() - t
+
+    mid = S // 2
+    rows = 64
+    t = run(mid, mid + rows)
+    rows = int(min(S - mid, max(rows, rows * budget_s / max(t, 1e-3))))
+    rows = max(bs, (rows // bs) * bs)
+    secs = run(mid, mid + rows)
+    pairs = 0
+    for i in range(mid, mid + rows):
+        hi = i if cfg["causal"] else S - 1
+        lo = max(0, i - cfg["window"] + 1) if cfg["window"] else 0
+        pairs += hi - lo + 1
+    flops = 4.0 * D * pairs
+    return {
+        "value": flops / secs / 1e12,
+        "unit": "TFLOP/s",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": (f"oracle/reference_forward.flash_attn_cpu_forward (numpy fp32), batch 0 "
+                   f"head 0, query rows [{mid}, {mid + rows}) of S={S}, block {bs} as the "
+                   f"reference dispatcher picks; {secs:.1f} s, {flops:.3e} FLOP; "
+                   f"os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def bench_prefill(name: str, steps: int, warmup: int, cpu_budget: float):
+    import torch
+
+    import fastest_flash_attention_amd as ffa
+
+    cfg = PREFILL[name]
+    B, Hq, Hkv, S, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
+    g = torch.Generator().manual_seed(0)
+    # BASELINE recipe: fp32 randn on the host in the order q, k, v, cast to bf16 on the
+    # host (identical bits on both sides), then moved to HBM.
+    q = torch.randn(B, Hq, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    kw = dict(causal=cfg["causal"], sliding_window=cfg["window"], softcap=cfg["softcap"])
+    if Hq != Hkv:
+        kw["num_kv_heads"] = Hkv
+
+    def step():
+        ffa.fastest_flash_attn_forward(qd, kd, vd, **kw)
+
+    ms_event, ms_wall = time_steps(step, steps, warmup)
+    pairs = n_valid_pairs_fast(S, cfg["causal"], cfg["window"])
+    flops = 4.0 * B * Hq * D * pairs
+    achieved = flops / (ms_event * 1e-3) / 1e12
+    cpu = cpu_baseline_prefill(cfg, q, k, v, cpu_budget) if cpu_budget > 0 else None
+    return {
+        "ms_per_step": ms_wall,
+        "kernel_ms": ms_event,
+        "value": flops / (ms_wall * 1e-3) / 1e12,
+        "flops": flops,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_BF16_TFLOPS,
+            "traffic": None,
+        },
+        "config": {"workload": f"{name}_prefill", "batch": B, "heads_q": Hq, "heads_kv": Hkv,
+                   "seq_len": S, "head_dim": D, "causal": cfg["causal"],
+                   "sliding_window": cfg["window"], "softcap": cfg["softcap"],
+                   "n_valid_pairs_per_head": pairs},
+        "cpu_baseline": cpu,
+    }
+
+
+def bench_decode(steps: int, warmup: int):
+    import torch
+
+    import fastest_flash_attention_amd as ffa
+
+    B, Hq, Hkv, D, P = 64, 32, 8, 128, 16
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 32769, (B,), generator=g)
+    pages = (lens + P - 1) // P
+    total = int(pages.sum())
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    bt = torch.zeros(B, int(pages.max()), dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        n = int(pages[b])
+        bt[b, :n] = perm[off:off + n]
+        off += n
+    # the 2 x 2.2 GB pools are drawn on the device (seeded) to keep host time short
+    gd = torch.Generator(device="cuda").manual_seed(0)
+    k_pages = torch.randn(total, Hkv, P, D, generator=gd, device="cuda").to(torch.bfloat16)
+    v_pages = torch.randn(total, Hkv, P, D, generator=gd, device="cuda").to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=gd, device="cuda").to(torch.bfloat16)
+    btd, lensd = bt.cuda(), lens.to(torch.int32).cuda()
+    max_len = int(lens.max())
+
+    def step():
+        ffa.fastest_flash_paged_decode(q, k_pages, v_pages, btd, lensd, return_lse=True,
+                                       max_context_len=max_len)
+
+    ms_event, ms_wall = time_steps(step, steps, warmup)
+    kv_bytes = int(lens.sum()) * Hkv * D * 2 * 2
+    nbytes = kv_bytes + 2 * B * Hq * D * 2 + B * Hq * 4 + int(pages.sum()) * 4 + B * 4
+    achieved = nbytes / (ms_event * 1e-3) / 1e9
+    return {
+        "metric": "paged-decode HBM GB/s",
+        "value": nbytes / (ms_wall * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "ms_per_step": ms_wall,
+        "kernel_ms": ms_event,
+        "bytes": nbytes,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None},
+        "config": {"workload": "cfg4_paged_decode", "batch": B, "heads_q": Hq, "heads_kv": Hkv,
+                   "head_dim": D, "page_size": P, "context_lens": "U[512, 32768] seed 0",
+                   "total_tokens": int(lens.sum())},
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="north_star", choices=sorted(PREFILL))
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="time budget of the CPU baseline sample (0 disables it)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU; --gpus must be 1 (the hot path "
+              "shards by (batch, head) with no exchange, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    pre = bench_prefill(args.workload, args.steps, args.warmup, args.cpu_seconds)
+    dec = None if args.no_decode else bench_decode(args.steps, args.warmup)
+    line = {
+        "metric": "prefill attn TFLOP/s (% bf16 MFMA peak); paged-decode HBM GB/s (% peak)",
+        "value": pre["value"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": pre["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1), no dataset)",
+        "config": pre["config"],
+        "roofline": pre["roofline"],
+        "cpu_baseline": pre["cpu_baseline"],
+        "decode": dec,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

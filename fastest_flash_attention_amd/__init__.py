@@ -1,0 +1,35 @@
+"""fastest_flash_attention_amd — MI355X-native forward attention.
+
+Drop-in for the forward hot path of MindIntels/fastest_flash_attention
+(reference __init__.py:40-88): the same functional entry point, modules, config and
+paged KV cache, with the GPU work done by hand-written gfx950 HIP kernels in
+libffa.so (C ABI: include/ffa.h).
+"""
+
+from .config import AttentionConfig
+from .modules import FastestFlashGQA, FastestFlashMHA, FastestFlashMLA
+from .ops import (
+    FastestFlashAttnFunc,
+    PagedKVCache,
+    fastest_flash_attn_forward,
+    fastest_flash_attn_func,
+    fastest_flash_paged_decode,
+)
+from .utils import auto_select_block_size, check_hip_available, check_triton_available
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "AttentionConfig",
+    "fastest_flash_attn_forward",
+    "fastest_flash_attn_func",
+    "FastestFlashAttnFunc",
+    "fastest_flash_paged_decode",
+    "FastestFlashMHA",
+    "FastestFlashGQA",
+    "FastestFlashMLA",
+    "PagedKVCache",
+    "auto_select_block_size",
+    "check_hip_available",
+    "check_triton_available",
+]

@@ -1,0 +1,134 @@
+// C-ABI entry points of libffa.so (declared in include/ffa.h).
+//
+// Every argument is validated on the host before any HIP call, so malformed calls
+// return an error code without touching the device; the kernels themselves then
+// only see shapes their grids and bounds checks were written for.
+
+#include <hip/hip_runtime.h>
+
+#include "ffa.h"
+#include "ffa_internal.h"
+
+namespace {
+
+bool valid_dtype(int32_t dt) { return dt == FFA_DTYPE_BF16 || dt == FFA_DTYPE_FP16; }
+
+}  // namespace
+
+extern "C" {
+
+int ffa_abi_version(void) { return FFA_ABI_VERSION; }
+
+const char* ffa_strerror(int status) {
+  switch (status) {
+    case FFA_OK:
+      return "ok";
+    case FFA_ERR_INVALID_ARG:
+      return "ffa: invalid argument (null pointer, non-positive size or bad stride)";
+    case FFA_ERR_UNSUPPORTED_DTYPE:
+      return "ffa: unsupported dtype (bfloat16 and float16 are supported)";
+    case FFA_ERR_UNSUPPORTED_HEAD_DIM:
+      return "ffa: unsupported head_dim (1..256 supported)";
+    case FFA_ERR_MISALIGNED:
+      return "ffa: misaligned operand";
+    case FFA_ERR_GQA_RATIO:
+      return "ffa: heads_q must be a positive multiple of heads_kv";
+    case FFA_ERR_WORKSPACE:
+      return "ffa: decode workspace missing or smaller than ffa_paged_decode_workspace_bytes()";
+    case FFA_ERR_LAUNCH:
+      return "ffa: kernel launch failed";
+    case FFA_ERR_NO_DEVICE:
+      return "ffa: no usable HIP device";
+    case FFA_ERR_TOO_LARGE:
+      return "ffa: problem size exceeds 32-bit grid/index limits";
+    default:
+      return "ffa: unknown error";
+  }
+}
+
+int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
+  if (a == nullptr) return FFA_ERR_INVALID_ARG;
+  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->seqlen_q < 0 || a->seqlen_kv < 0) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->heads_q % a->heads_kv != 0) return FFA_ERR_GQA_RATIO;
+  if (a->batch == 0 || a->seqlen_q == 0) return FFA_OK;
+  if (a->q == nullptr || a->o == nullptr) return FFA_ERR_INVALID_ARG;
+  if (a->seqlen_kv > 0 && (a->k == nullptr || a->v == nullptr)) return FFA_ERR_INVALID_ARG;
+  if (a->q_stride[3] != 1 || a->k_stride[3] != 1 || a->v_stride[3] != 1 || a->o_stride[3] != 1) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  for (int i = 0; i < 3; ++i) {
+    if (a->q_stride[i] < 0 || a->k_stride[i] < 0 || a->v_stride[i] < 0 || a->o_stride[i] < 0 ||
+        a->lse_stride[i] < 0) {
+      return FFA_ERR_INVALID_ARG;
+    }
+  }
+  if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  // Positions are int32 inside the kernel.
+  const int64_t max_pos = static_cast<int64_t>(a->q_offset) + a->seqlen_q;
+  if (max_pos > 0x3fffffff || a->seqlen_kv > 0x3fffffff || a->q_offset < -0x3fffffff) {
+    return FFA_ERR_TOO_LARGE;
+  }
+  return ffa::launch_prefill(*a, static_cast<hipStream_t>(stream));
+}
+
+int ffa_paged_gather(const ffa_paged_gather_args* a, void* stream) {
+  if (a == nullptr) return FFA_ERR_INVALID_ARG;
+  if (a->elem_bytes != 2 && a->elem_bytes != 4) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (a->heads_kv < 1 || a->page_size < 1 || a->head_dim < 1 || a->context_len < 0 ||
+      a->num_pages < 0) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->context_len == 0) return FFA_OK;
+  if (a->k_pages == nullptr || a->v_pages == nullptr || a->k_out == nullptr ||
+      a->v_out == nullptr || a->page_table == nullptr) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  return ffa::launch_paged_gather(*a, static_cast<hipStream_t>(stream));
+}
+
+int32_t ffa_paged_decode_num_splits(int32_t max_context_len, int32_t tokens_per_split) {
+  if (max_context_len < 0) return 0;
+  return ffa::decode_num_splits(max_context_len, tokens_per_split);
+}
+
+size_t ffa_paged_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
+                                        int32_t max_context_len, int32_t tokens_per_split) {
+  if (batch < 0 || heads_q < 0 || head_dim < 0 || max_context_len < 0) return 0;
+  return ffa::decode_workspace_bytes(batch, heads_q, head_dim, max_context_len, tokens_per_split);
+}
+
+int ffa_paged_decode_fwd(const ffa_paged_decode_args* a, void* stream) {
+  if (a == nullptr) return FFA_ERR_INVALID_ARG;
+  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->page_size < 1 ||
+      a->num_pages < 0 || a->max_context_len < 0 || a->tokens_per_split < 0) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->heads_q % a->heads_kv != 0) return FFA_ERR_GQA_RATIO;
+  if (a->heads_q / a->heads_kv > 64) return FFA_ERR_GQA_RATIO;
+  if (a->batch == 0) return FFA_OK;
+  if (a->q == nullptr || a->o == nullptr || a->k_pages == nullptr || a->v_pages == nullptr ||
+      a->block_tables == nullptr || a->context_lens == nullptr) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  const int64_t max_blocks =
+      (static_cast<int64_t>(a->max_context_len) + a->page_size - 1) / a->page_size;
+  if (a->block_table_stride < max_blocks) return FFA_ERR_INVALID_ARG;
+  for (int i = 0; i < 2; ++i) {
+    if (a->q_stride[i] < 0 || a->o_stride[i] < 0 || a->lse_stride[i] < 0) {
+      return FFA_ERR_INVALID_ARG;
+    }
+  }
+  if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  const size_t need = ffa::decode_workspace_bytes(a->batch, a->heads_q, a->head_dim,
+                                                  a->max_context_len, a->tokens_per_split);
+  if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need)) return FFA_ERR_WORKSPACE;
+  return ffa::launch_paged_decode(*a, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

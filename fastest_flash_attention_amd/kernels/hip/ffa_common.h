@@ -1,0 +1,125 @@
+// Shared device helpers of the gfx950 attention kernels: operand vector types,
+// MFMA wrappers, 16-bit element conversion and guarded row loads.
+//
+// MFMA v_mfma_f32_32x32x16_{bf16,f16} operand layout (wave64, lane l, g = l / 32):
+//   A [32 x 16] : lane l holds A[l % 32][8g .. 8g+7]
+//   B [16 x 32] : lane l holds B[8g .. 8g+7][l % 32]
+//   C [32 x 32] : lane l holds C[8i + 4g + j][l % 32] in acc[4i + j], i, j in 0..3
+// (checked on the device by tests/test_gpu_mfma_layout.py).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ffa {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+
+// Element tags: 16-bit storage types the kernels accept.
+struct Bf16Tag {};
+struct F16Tag {};
+
+template <typename Tag>
+struct Elem;
+
+template <>
+struct Elem<Bf16Tag> {
+  // 32x32x16 MFMA on raw 16-bit patterns.
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // Two fp32 -> packed pair (x in the low half), round to nearest even.
+  __device__ static inline uint32_t pack2(float x, float y) {
+    f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  }
+  __device__ static inline float to_f32(uint16_t h) {
+    return __builtin_bit_cast(float, static_cast<uint32_t>(h) << 16);
+  }
+};
+
+template <>
+struct Elem<F16Tag> {
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline uint32_t pack2(float x, float y) {
+    f32x2 v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+  __device__ static inline float to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  }
+};
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// tanh(y) = sign(y) * (1 - e) / (1 + e), e = exp(-2|y|); |error| ~ 1e-7 absolute.
+__device__ inline float tanh_approx(float y) {
+  const float e = fast_exp2(fabsf(y) * (-2.0f * kLog2e));
+  const float t = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+  return __builtin_copysignf(t, y);
+}
+
+// Eight consecutive 16-bit elements row[d0 .. d0+7] as one 128-bit value, zero
+// beyond `dlim`. `vec` promises 16-byte alignment of row + d0 whenever d0 + 8 <= dlim.
+__device__ inline u32x4 load_row8(const uint16_t* __restrict__ row, int d0, int dlim, bool vec) {
+  if (vec && d0 + 8 <= dlim) {
+    return *reinterpret_cast<const u32x4*>(row + d0);
+  }
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (d0 + e < dlim) {
+      w[e >> 1] |= static_cast<uint32_t>(row[d0 + e]) << ((e & 1) * 16);
+    }
+  }
+  u32x4 r = {w[0], w[1], w[2], w[3]};
+  return r;
+}
+
+// Interleave four key rows (8 dims each) into key-quad order: for every dim d the
+// output holds keys 0..3 contiguously (8 bytes). out[2*dd + 0] = (key0, key1) of
+// dim dd, out[2*dd + 1] = (key2, key3) of dim dd.
+__device__ inline void quad_interleave(const u32x4& r0, const u32x4& r1, const u32x4& r2,
+                                       const u32x4& r3, u32x4 out[4]) {
+  uint32_t o[16];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    o[4 * w + 0] = (r0[w] & 0xffffu) | (r1[w] << 16);
+    o[4 * w + 1] = (r2[w] & 0xffffu) | (r3[w] << 16);
+    o[4 * w + 2] = (r0[w] >> 16) | (r1[w] & 0xffff0000u);
+    o[4 * w + 3] = (r2[w] >> 16) | (r3[w] & 0xffff0000u);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[i] = u32x4{o[4 * i + 0], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]};
+  }
+}
+
+__device__ inline float wave_xor32(float x) { return __shfl_xor(x, 32); }
+
+}  // namespace ffa

@@ -1,0 +1,538 @@
+// Paged KV decode and paged gather for gfx950.
+//
+// Pool layout and index law of PagedKVCache (reference ops/kv_cache.py:142-149,194-203):
+// pages [num_pages, heads_kv, page_size, head_dim]; token t of a sequence lives in
+// physical page block_table[t / page_size], slot t % page_size.
+//
+// Decode (one query token per sequence, GQA group of G = Hq / Hkv query heads per KV
+// head) is split-K:
+//   split kernel  grid (splits, Hkv * column_groups, batch), 4 waves per workgroup.
+//                 A workgroup streams tokens_per_split tokens of one (sequence, KV head)
+//                 straight from the pages; every K/V byte is read once and serves all
+//                 G query heads of the group (no repeat_kv).
+//                 Per 32-token tile, wave-level:
+//                   S^T[key, head] = K Q^T    v_mfma_f32_16x16x32: K (A operand) is
+//                                  loaded from HBM directly in operand layout: a lane
+//                                  reads 16 B of one token row, 16 lanes cover 16 rows x
+//                                  64 B, so every 128-bit load is fully used;
+//                   softmax        fp32, exp2, max/sum via lane swaps (xor 16, 32),
+//                                  rescale deferred until the max grows by 2^8;
+//                   O^T += V^T P^T V staged through a per-wave LDS region in key-quad
+//                                  order ([key/4][dim][4 keys]) so its A operand is two
+//                                  8-byte LDS reads; P comes straight from the S^T
+//                                  accumulators.
+//                 The next tile's K/V loads are issued before the current tile is
+//                 computed. The 4 waves' partials are merged through LDS and one
+//                 normalised (O, lse) partial per query head goes to the workspace.
+//   combine kernel one wave per (sequence, query head): O = sum_s exp(lse_s - lse) O_s,
+//                 lse = logsumexp_s lse_s.
+// Page ids outside [0, num_pages) read as zeros instead of faulting.
+
+#include "ffa_common.h"
+#include "ffa_internal.h"
+
+namespace ffa {
+namespace {
+
+constexpr int kDecThreads = 256;
+constexpr int kDecWaves = 4;
+constexpr int kTile = 32;            // tokens per wave tile
+constexpr int kCols = 16;            // query heads per workgroup (MFMA N)
+constexpr int kDefaultSplit = 512;   // tokens per split
+constexpr int kMinSplit = 32;
+constexpr float kRescaleThresh = 8.0f;
+
+struct DecodeParams {
+  const uint16_t* q;
+  const uint16_t* kp;
+  const uint16_t* vp;
+  uint16_t* o;
+  float* lse;
+  const int32_t* bt;
+  const int32_t* lens;
+  float* ws_o;    // [B][Hq][n_splits][DP]
+  float* ws_lse;  // [B][Hq][n_splits]
+  int64_t q_sb, q_sh, o_sb, o_sh, l_sb, l_sh;
+  int64_t page_stride;  // Hkv * P * D elements
+  int64_t head_stride;  // P * D elements
+  int bt_stride;
+  int B, Hq, Hkv, G, D, P, log2P, num_pages;
+  int n_splits, tps, window;
+  int max_len;  // context lengths are clamped to this (it sizes the grid)
+  int n_cg;
+  int dp;
+  float score_mul, cap_mul;
+  int vec;
+};
+
+template <int DP>
+struct DShape {
+  static constexpr int KS = DP / 32;          // k-steps of the 16x16x32 QK product
+  static constexpr int DB = DP / 16;          // 16-dim blocks of O^T
+  static constexpr int VSTR = DP * 4;         // key-quad row stride (16-bit elements)
+  static constexpr int V_ELEMS = (kTile / 4) * VSTR;  // per wave
+  static constexpr int VITEMS = (kTile / 4) * (DP / 8);
+  static constexpr int VPL = (VITEMS + 63) / 64;      // items per lane
+};
+
+__device__ inline int page_of(const DecodeParams& p, int tok, int& slot) {
+  if (p.log2P >= 0) {
+    slot = tok & (p.P - 1);
+    return tok >> p.log2P;
+  }
+  const int pi = tok / p.P;
+  slot = tok - pi * p.P;
+  return pi;
+}
+
+// Row pointer of token `tok` (must be < context length) in `pool`, or nullptr when
+// the block table names a page outside the pool.
+__device__ inline const uint16_t* token_row(const DecodeParams& p, const uint16_t* pool,
+                                            const int32_t* btrow, int hk, int tok) {
+  int slot;
+  const int pi = page_of(p, tok, slot);
+  const int phys = btrow[pi];
+  if (phys < 0 || phys >= p.num_pages) return nullptr;
+  return pool + static_cast<int64_t>(phys) * p.page_stride + hk * p.head_stride +
+         static_cast<int64_t>(slot) * p.D;
+}
+
+// head_dim <= 128: two workgroups per CU; wider heads keep twice the K/V tile in
+// registers and run one wave per SIMD.
+template <int DP>
+constexpr int kDecMinBlocks = DP <= 128 ? 2 : 1;
+
+template <typename Tag, int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_kernel(
+    const DecodeParams p) {
+  using S = DShape<DP>;
+  using E = Elem<Tag>;
+  // V staging during the sweep; reused for the wave merge afterwards.
+  constexpr int kVBytes = kDecWaves * S::V_ELEMS * 2;
+  constexpr int kRedBytes = kDecWaves * kCols * (DP + 1) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kVBytes > kRedBytes ? kVBytes : kRedBytes];
+  __shared__ float red_m[kDecWaves][kCols];
+  __shared__ float red_l[kDecWaves][kCols];
+  auto red_o = reinterpret_cast<float(*)[kCols][DP + 1]>(smem);
+
+  const int split = blockIdx.x;
+  const int hk = blockIdx.y / p.n_cg;
+  const int cg = blockIdx.y - hk * p.n_cg;
+  const int b = blockIdx.z;
+  const int L = min(max(p.lens[b], 0), p.max_len);
+  const int lo = p.window > 0 ? max(0, L - p.window) : 0;
+  const int s_begin = max(split * p.tps, lo);
+  const int s_end = min(split * p.tps + p.tps, L);
+  if (s_begin >= s_end) return;  // uniform across the workgroup: no barrier reached
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int c16 = lane & 15;  // MFMA column = query head within the group
+  const int g4 = lane >> 4;   // 0..3
+  const int gcols = min(kCols, p.G - cg * kCols);
+  const int head0 = hk * p.G + cg * kCols;
+  const bool col_live = c16 < gcols;
+  const bool vec = p.vec != 0;
+  const int D = p.D;
+  const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+
+  // Q^T as the B operand: lane holds head (head0 + c16), dims 32*ks + 8*g4 .. +7.
+  u32x4 qreg[S::KS];
+  {
+    const uint16_t* qr = p.q + b * p.q_sb + (head0 + c16) * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < S::KS; ++ks) {
+      qreg[ks] = col_live ? load_row8(qr, 32 * ks + 8 * g4, D, vec) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  f32x4 oacc[S::DB];
+#pragma unroll
+  for (int db = 0; db < S::DB; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf;
+  float l_run = 0.0f;
+
+  const int n_tiles = (s_end - s_begin + kTile - 1) / kTile;
+  uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + wave * S::V_ELEMS;
+
+  u32x4 kreg[2][S::KS];
+  u32x4 vreg[S::VPL][4];
+
+  auto gload = [&](int it) {
+    const int t0 = s_begin + it * kTile;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int tok = t0 + 16 * sub + c16;
+      const uint16_t* row = tok < s_end ? token_row(p, p.kp, btrow, hk, tok) : nullptr;
+#pragma unroll
+      for (int ks = 0; ks < S::KS; ++ks) {
+        kreg[sub][ks] =
+            row != nullptr ? load_row8(row, 32 * ks + 8 * g4, D, vec) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < S::VPL; ++i) {
+      const int item = lane + 64 * i;
+      if (item < S::VITEMS) {
+        const int kq = item / (DP / 8);
+        const int c8 = item - kq * (DP / 8);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = t0 + 4 * kq + r;
+          const uint16_t* row = tok < s_end ? token_row(p, p.vp, btrow, hk, tok) : nullptr;
+          vreg[i][r] = row != nullptr ? load_row8(row, c8 * 8, D, vec) : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+  };
+
+  int it = wave;
+  if (it < n_tiles) gload(it);
+  for (; it < n_tiles; it += kDecWaves) {
+    // V of this tile -> LDS (key quads); K of this tile stays in registers.
+#pragma unroll
+    for (int i = 0; i < S::VPL; ++i) {
+      const int item = lane + 64 * i;
+      if (item < S::VITEMS) {
+        const int kq = item / (DP / 8);
+        const int c8 = item - kq * (DP / 8);
+        u32x4 out[4];
+        quad_interleave(vreg[i][0], vreg[i][1], vreg[i][2], vreg[i][3], out);
+        u32x4* dst = reinterpret_cast<u32x4*>(vl + kq * S::VSTR + c8 * 32);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) dst[w] = out[w];
+      }
+    }
+    u32x4 kc[2][S::KS];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int ks = 0; ks < S::KS; ++ks) kc[sub][ks] = kreg[sub][ks];
+    }
+    const int t0 = s_begin + it * kTile;
+    if (it + kDecWaves < n_tiles) gload(it + kDecWaves);
+
+    f32x4 sacc[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      sacc[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < S::KS; ++ks) sacc[sub] = E::mfma16(kc[sub][ks], qreg[ks], sacc[sub]);
+    }
+    float mt = kNegInf;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float x = sacc[sub][j];
+        if constexpr (SOFTCAP) {
+          x = p.cap_mul * tanh_approx(x * p.score_mul);
+        } else {
+          x = x * p.score_mul;
+        }
+        const int tok = t0 + 16 * sub + 4 * g4 + j;
+        x = (tok < s_end) ? x : kNegInf;  // tokens below `lo` never enter a split range
+        sacc[sub][j] = x;
+        mt = fmaxf(mt, x);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const bool need = m_new > m_run + kRescaleThresh;
+    if (__any(need)) {
+      const float alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
+      m_run = need ? m_new : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < S::DB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) oacc[db][j] *= alpha;
+      }
+    }
+    const float mu = (m_run == kNegInf) ? 0.0f : m_run;
+    float pv[8];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pv[4 * sub + j] = fast_exp2(sacc[sub][j] - mu);
+        l_run += pv[4 * sub + j];
+      }
+    }
+    const u32x4 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
+                      E::pack2(pv[6], pv[7])};
+#pragma unroll
+    for (int db = 0; db < S::DB; ++db) {
+      const int d = 16 * db + c16;
+      const u32x2 a0 = *reinterpret_cast<const u32x2*>(vl + g4 * S::VSTR + d * 4);
+      const u32x2 a1 = *reinterpret_cast<const u32x2*>(vl + (4 + g4) * S::VSTR + d * 4);
+      const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
+      oacc[db] = E::mfma16(a, pk, oacc[db]);
+    }
+  }
+
+  // Per-wave totals, then merge the 4 waves through LDS.
+  float l_w = l_run + __shfl_xor(l_run, 16);
+  l_w += __shfl_xor(l_w, 32);
+  __syncthreads();  // every wave is done with its V staging region
+  if (g4 == 0) {
+    red_m[wave][c16] = m_run;
+    red_l[wave][c16] = l_w;
+  }
+#pragma unroll
+  for (int db = 0; db < S::DB; ++db) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red_o[wave][c16][16 * db + 4 * g4 + j] = oacc[db][j];
+  }
+  __syncthreads();
+
+  // thread -> (column, dim) pairs of the merged partial
+  for (int idx = tid; idx < kCols * DP; idx += kDecThreads) {
+    const int n = idx / DP;
+    const int d = idx - n * DP;
+    if (n >= gcols) continue;
+    float mm = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) mm = fmaxf(mm, red_m[w][n]);
+    float lsum = 0.0f;
+    float osum = 0.0f;
+    if (mm != kNegInf) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const float wt = fast_exp2(red_m[w][n] - mm);
+        lsum += wt * red_l[w][n];
+        osum += wt * red_o[w][n][d];
+      }
+    }
+    const int hq = head0 + n;
+    const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hq) * p.n_splits + split;
+    if (d < D) p.ws_o[slot * p.dp + d] = lsum > 0.0f ? osum / lsum : 0.0f;
+    if (d == 0) p.ws_lse[slot] = lsum > 0.0f ? (mm + fast_log2(lsum)) * kLn2 : kNegInf;
+  }
+}
+
+template <typename Tag>
+__global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p) {
+  using E = Elem<Tag>;
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hq;
+  const int hq = bh - b * p.Hq;
+  const int lane = threadIdx.x;
+  const int L = min(max(p.lens[b], 0), p.max_len);
+  const int lo = p.window > 0 ? max(0, L - p.window) : 0;
+  const int s0 = lo / p.tps;
+  const int s1 = L > 0 ? (L + p.tps - 1) / p.tps : 0;
+  const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.n_splits;
+
+  float mm = kNegInf;
+  for (int s = s0 + lane; s < s1; s += 64) mm = fmaxf(mm, p.ws_lse[base + s]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
+
+  float wsum = 0.0f;
+  if (mm != kNegInf) {
+    for (int s = s0 + lane; s < s1; s += 64) wsum += __expf(p.ws_lse[base + s] - mm);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) wsum += __shfl_xor(wsum, off);
+
+  uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh;
+  for (int d = lane; d < p.D; d += 64) {
+    float acc = 0.0f;
+    if (mm != kNegInf) {
+      for (int s = s0; s < s1; ++s) {
+        const float ls = p.ws_lse[base + s];
+        if (ls != kNegInf) acc += __expf(ls - mm) * p.ws_o[(base + s) * p.dp + d];
+      }
+      acc = acc / wsum;
+    }
+    const uint32_t w = E::pack2(acc, 0.0f);
+    orow[d] = static_cast<uint16_t>(w & 0xffffu);
+  }
+  if (lane == 0 && p.lse != nullptr) {
+    p.lse[b * p.l_sb + hq * p.l_sh] = (mm != kNegInf && wsum > 0.0f) ? mm + logf(wsum) : kNegInf;
+  }
+}
+
+// get_kv: copy the first context_len tokens of one sequence into [H, L, D].
+template <typename U>
+__global__ __launch_bounds__(256) void paged_gather_kernel(const U* __restrict__ kp,
+                                                           const U* __restrict__ vp,
+                                                           U* __restrict__ ko, U* __restrict__ vo,
+                                                           const int32_t* __restrict__ pt,
+                                                           int num_pages, int H, int P,
+                                                           int row_units, int L) {
+  const int64_t total = static_cast<int64_t>(H) * L * row_units;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int u = static_cast<int>(i % row_units);
+    const int64_t ht = i / row_units;
+    const int t = static_cast<int>(ht % L);
+    const int h = static_cast<int>(ht / L);
+    const int phys = pt[t / P];
+    const int slot = t - (t / P) * P;
+    U kv = U{};
+    U vv = U{};
+    if (phys >= 0 && phys < num_pages) {
+      const int64_t src = ((static_cast<int64_t>(phys) * H + h) * P + slot) * row_units + u;
+      kv = kp[src];
+      vv = vp[src];
+    }
+    ko[i] = kv;
+    vo[i] = vv;
+  }
+}
+
+template <typename Tag, int DP>
+void launch_decode_dp(const DecodeParams& p, bool softcap, dim3 grid, hipStream_t s) {
+  if (softcap) {
+    hipLaunchKernelGGL((decode_split_kernel<Tag, DP, true>), grid, dim3(kDecThreads), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((decode_split_kernel<Tag, DP, false>), grid, dim3(kDecThreads), 0, s, p);
+  }
+}
+
+template <typename Tag>
+void launch_decode_tag(DecodeParams& p, bool softcap, dim3 grid, hipStream_t s) {
+  if (p.D <= 32) {
+    p.dp = 32;
+    launch_decode_dp<Tag, 32>(p, softcap, grid, s);
+  } else if (p.D <= 64) {
+    p.dp = 64;
+    launch_decode_dp<Tag, 64>(p, softcap, grid, s);
+  } else if (p.D <= 128) {
+    p.dp = 128;
+    launch_decode_dp<Tag, 128>(p, softcap, grid, s);
+  } else if (p.D <= 192) {
+    p.dp = 192;
+    launch_decode_dp<Tag, 192>(p, softcap, grid, s);
+  } else {
+    p.dp = 256;
+    launch_decode_dp<Tag, 256>(p, softcap, grid, s);
+  }
+  hipLaunchKernelGGL((decode_combine_kernel<Tag>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
+}
+
+int dp_of(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : d <= 192 ? 192 : 256; }
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+}  // namespace
+
+int32_t decode_tokens_per_split(int32_t tokens_per_split) {
+  if (tokens_per_split <= 0) return kDefaultSplit;
+  const int32_t t = ((tokens_per_split + kTile - 1) / kTile) * kTile;
+  return t < kMinSplit ? kMinSplit : t;
+}
+
+int32_t decode_num_splits(int32_t max_context_len, int32_t tokens_per_split) {
+  const int32_t tps = decode_tokens_per_split(tokens_per_split);
+  return max_context_len <= 0 ? 1 : (max_context_len + tps - 1) / tps;
+}
+
+size_t decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
+                              int32_t max_context_len, int32_t tokens_per_split) {
+  const size_t ns = static_cast<size_t>(decode_num_splits(max_context_len, tokens_per_split));
+  const size_t rows = static_cast<size_t>(batch) * heads_q * ns;
+  return rows * (static_cast<size_t>(dp_of(head_dim)) + 1) * sizeof(float);
+}
+
+int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream) {
+  DecodeParams p{};
+  p.q = static_cast<const uint16_t*>(a.q);
+  p.kp = static_cast<const uint16_t*>(a.k_pages);
+  p.vp = static_cast<const uint16_t*>(a.v_pages);
+  p.o = static_cast<uint16_t*>(a.o);
+  p.lse = a.lse;
+  p.bt = a.block_tables;
+  p.lens = a.context_lens;
+  p.B = a.batch;
+  p.Hq = a.heads_q;
+  p.Hkv = a.heads_kv;
+  p.G = a.heads_q / a.heads_kv;
+  p.D = a.head_dim;
+  p.P = a.page_size;
+  p.log2P = ((a.page_size & (a.page_size - 1)) == 0) ? __builtin_ctz(a.page_size) : -1;
+  p.num_pages = a.num_pages;
+  p.tps = decode_tokens_per_split(a.tokens_per_split);
+  p.n_splits = decode_num_splits(a.max_context_len, a.tokens_per_split);
+  p.window = a.window > 0 ? a.window : 0;
+  p.max_len = a.max_context_len;
+  p.n_cg = (p.G + kCols - 1) / kCols;
+  p.dp = dp_of(a.head_dim);
+  p.q_sb = a.q_stride[0];
+  p.q_sh = a.q_stride[1];
+  p.o_sb = a.o_stride[0];
+  p.o_sh = a.o_stride[1];
+  p.l_sb = a.lse_stride[0];
+  p.l_sh = a.lse_stride[1];
+  p.page_stride = static_cast<int64_t>(a.heads_kv) * a.page_size * a.head_dim;
+  p.head_stride = static_cast<int64_t>(a.page_size) * a.head_dim;
+  p.bt_stride = a.block_table_stride;
+  const bool softcap = a.softcap > 0.0f;
+  if (softcap) {
+    p.score_mul = a.scale / a.softcap;
+    p.cap_mul = a.softcap * kLog2e;
+  } else {
+    p.score_mul = a.scale * kLog2e;
+    p.cap_mul = 0.0f;
+  }
+  const bool vec = (a.head_dim % 8) == 0 && aligned16(a.q) && aligned16(a.k_pages) &&
+                   aligned16(a.v_pages) && (a.q_stride[0] % 8) == 0 && (a.q_stride[1] % 8) == 0;
+  p.vec = vec ? 1 : 0;
+  const size_t rows = static_cast<size_t>(a.batch) * a.heads_q * p.n_splits;
+  p.ws_o = static_cast<float*>(a.workspace);
+  p.ws_lse = p.ws_o + rows * p.dp;
+
+  const int64_t gy = static_cast<int64_t>(a.heads_kv) * p.n_cg;
+  if (gy > 65535 || a.batch > 65535 || static_cast<int64_t>(a.batch) * a.heads_q > 0x7fffffff) {
+    return FFA_ERR_TOO_LARGE;
+  }
+  const dim3 grid(p.n_splits, static_cast<unsigned>(gy), a.batch);
+  if (a.dtype == FFA_DTYPE_BF16) {
+    launch_decode_tag<Bf16Tag>(p, softcap, grid, stream);
+  } else {
+    launch_decode_tag<F16Tag>(p, softcap, grid, stream);
+  }
+  return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
+}
+
+int launch_paged_gather(const ffa_paged_gather_args& a, hipStream_t stream) {
+  const int64_t row_bytes = static_cast<int64_t>(a.head_dim) * a.elem_bytes;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(a.k_pages) |
+                          reinterpret_cast<uintptr_t>(a.v_pages) |
+                          reinterpret_cast<uintptr_t>(a.k_out) |
+                          reinterpret_cast<uintptr_t>(a.v_out);
+  const int64_t units_total = static_cast<int64_t>(a.heads_kv) * a.context_len;
+  auto grid_for = [&](int64_t units) {
+    const int64_t blocks = (units + 255) / 256;
+    return static_cast<unsigned>(blocks < 65536 ? (blocks < 1 ? 1 : blocks) : 65536);
+  };
+  if (row_bytes % 16 == 0 && (align & 15u) == 0) {
+    const int ru = static_cast<int>(row_bytes / 16);
+    hipLaunchKernelGGL(paged_gather_kernel<u32x4>, dim3(grid_for(units_total * ru)), dim3(256), 0,
+                       stream, static_cast<const u32x4*>(a.k_pages),
+                       static_cast<const u32x4*>(a.v_pages), static_cast<u32x4*>(a.k_out),
+                       static_cast<u32x4*>(a.v_out), a.page_table, a.num_pages, a.heads_kv,
+                       a.page_size, ru, a.context_len);
+  } else if (row_bytes % 4 == 0 && (align & 3u) == 0) {
+    const int ru = static_cast<int>(row_bytes / 4);
+    hipLaunchKernelGGL(paged_gather_kernel<uint32_t>, dim3(grid_for(units_total * ru)), dim3(256),
+                       0, stream, static_cast<const uint32_t*>(a.k_pages),
+                       static_cast<const uint32_t*>(a.v_pages), static_cast<uint32_t*>(a.k_out),
+                       static_cast<uint32_t*>(a.v_out), a.page_table, a.num_pages, a.heads_kv,
+                       a.page_size, ru, a.context_len);
+  } else {
+    const int ru = static_cast<int>(row_bytes / 2);
+    hipLaunchKernelGGL(paged_gather_kernel<uint16_t>, dim3(grid_for(units_total * ru)), dim3(256),
+                       0, stream, static_cast<const uint16_t*>(a.k_pages),
+                       static_cast<const uint16_t*>(a.v_pages), static_cast<uint16_t*>(a.k_out),
+                       static_cast<uint16_t*>(a.v_out), a.page_table, a.num_pages, a.heads_kv,
+                       a.page_size, ru, a.context_len);
+  }
+  return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
+}
+
+}  // namespace ffa

@@ -1,0 +1,24 @@
+// Internal launch interface between the C-ABI layer (ffa_api.hip) and the kernel
+// translation units. Arguments arrive here already validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "ffa.h"
+
+namespace ffa {
+
+// Prefill: one launch of the fused forward kernel.
+int launch_prefill(const ffa_prefill_args& a, hipStream_t stream);
+
+// Paged decode: split kernel + logsumexp combine kernel.
+int32_t decode_num_splits(int32_t max_context_len, int32_t tokens_per_split);
+int32_t decode_tokens_per_split(int32_t tokens_per_split);
+size_t decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
+                              int32_t max_context_len, int32_t tokens_per_split);
+int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream);
+
+// get_kv gather.
+int launch_paged_gather(const ffa_paged_gather_args& a, hipStream_t stream);
+
+}  // namespace ffa

@@ -1,0 +1,284 @@
+"""fastest_flash_attn_forward — the drop-in forward entry point.
+
+Argument handling mirrors the reference dispatcher (ops/attention_forward.py:23-167):
+config precedence (:66-73), 3D -> 4D (:76), kv_cache concatenation with
+``q_offset = S_kv_total - S_q`` (:82-89), GQA (:94-96), default scale (:98-99) and
+block-size resolution (:102-109). The dispatch (:112-159) is replaced by a single
+path: one call of ``ffa_prefill_fwd`` in libffa.so (hand-written gfx950 HIP) on the
+current HIP stream. There is no Triton, no autotuner, no alternative GPU kernel and
+no CPU fallback: non-ROCm tensors, unsupported dtypes or features raise.
+
+GQA is applied by index inside the kernel (q head h reads kv head h // (Hq // Hkv)),
+so ``num_kv_heads`` costs no ``repeat_kv`` copy. The block size only selects the
+reference tiling that defines the LSE of rows with no visible key; the kernel's own
+tiles do not change any other result.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from ..config import AttentionConfig
+from ..kernels import _lib
+from ..utils import auto_select_block_size, maybe_unsqueeze_head
+
+
+@dataclass
+class ResolvedForward:
+    """Arguments after the reference dispatcher's resolution (host logic only)."""
+
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    B: int
+    H_q: int
+    H_kv: int
+    S_q: int
+    S_kv: int
+    D: int
+    q_offset: int
+    scale: float
+    causal: bool
+    sliding_window: Optional[int]
+    softcap: Optional[float]
+    two_pass: bool
+    compute_dtype: Optional[torch.dtype]
+    block_mask: Optional[torch.Tensor]
+    block_q: int
+    block_kv: int
+    return_lse: bool
+    squeezed: bool
+
+
+@dataclass
+class PrefillCall:
+    """A fully resolved prefill launch: the ABI struct plus the tensors it points to."""
+
+    args: _lib.PrefillArgs
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    out: torch.Tensor
+    lse: Optional[torch.Tensor]
+    squeezed: bool
+
+
+def _unit_last(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 or t.size(-1) == 1 else t.contiguous()
+
+
+def _batch_strides(t: torch.Tensor, B: int, name: str) -> list[int]:
+    """[b, h, s, d] element strides; a size-1 batch broadcasts against B (torch.matmul
+    broadcasting in the reference CPU path)."""
+    st = list(t.stride())
+    if t.size(0) != B:
+        if t.size(0) != 1:
+            raise ValueError(f"{name} batch {t.size(0)} does not match q batch {B}")
+        st[0] = 0
+    if t.size(-1) == 1:
+        st[3] = 1
+    return st
+
+
+def resolve_forward_args(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    config: Optional[AttentionConfig] = None,
+    *,
+    scale: Optional[float] = None,
+    causal: bool = False,
+    block_size: Optional[int] = None,
+    block_mask: Optional[torch.Tensor] = None,
+    softcap: Optional[float] = None,
+    sliding_window: Optional[int] = None,
+    two_pass: bool = False,
+    compute_dtype: Optional[torch.dtype] = None,
+    num_kv_heads: Optional[int] = None,
+    kv_cache: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+    return_lse: bool = False,
+) -> ResolvedForward:
+    """Argument resolution of the reference dispatcher (ops/attention_forward.py:65-109)."""
+    if config is not None:
+        causal = config.causal
+        softcap = config.softcap
+        sliding_window = config.sliding_window
+        two_pass = config.two_pass
+        compute_dtype = config.compute_dtype
+        num_kv_heads = config.num_kv_heads
+        return_lse = config.return_lse
+
+    q, k, v, squeezed = maybe_unsqueeze_head(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 3D [B, S, D] or 4D [B, H, S, D]")
+    B, H_q, S_q, D = q.shape
+    H_kv = k.size(1)
+
+    q_offset = 0
+    if kv_cache is not None:
+        k_cache, v_cache = kv_cache
+        if k_cache.dim() == 3:
+            k_cache = k_cache.unsqueeze(1)
+            v_cache = v_cache.unsqueeze(1)
+        k = torch.cat([k_cache, k], dim=2)
+        v = torch.cat([v_cache, v], dim=2)
+        q_offset = k.size(2) - S_q
+    S_kv = k.size(2)
+
+    if v.shape[:3] != k.shape[:3] or k.size(3) != D or v.size(3) != D:
+        raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
+    if H_q != H_kv:
+        if num_kv_heads is None and H_kv != 1:
+            raise ValueError(f"q has {H_q} heads and k/v have {H_kv}: pass num_kv_heads for GQA")
+        if H_q % H_kv != 0:
+            raise ValueError(f"num heads {H_q} is not a multiple of kv heads {H_kv}")
+    if sliding_window is not None and int(sliding_window) <= 0:
+        raise ValueError("sliding_window must be positive")
+    if softcap is not None and float(softcap) <= 0.0:
+        raise ValueError("softcap must be positive")
+
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+
+    if block_size is None:
+        if config is not None:
+            bq, bkv = config.resolve_block_sizes(S_q, S_kv, D)
+        else:
+            bq = bkv = auto_select_block_size(S_q, S_kv, D)
+    else:
+        bq = bkv = block_size
+
+    return ResolvedForward(
+        q=q, k=k, v=v, B=B, H_q=H_q, H_kv=H_kv, S_q=S_q, S_kv=S_kv, D=D,
+        q_offset=q_offset, scale=float(scale), causal=bool(causal),
+        sliding_window=None if sliding_window is None else int(sliding_window),
+        softcap=None if softcap is None else float(softcap), two_pass=bool(two_pass),
+        compute_dtype=compute_dtype, block_mask=block_mask, block_q=int(bq),
+        block_kv=int(bkv), return_lse=bool(return_lse), squeezed=squeezed,
+    )
+
+
+def build_prefill_args(
+    r: ResolvedForward, out: torch.Tensor, lse: Optional[torch.Tensor], dtype_code: int
+) -> _lib.PrefillArgs:
+    """Fill ``ffa_prefill_args`` from resolved arguments (no launch, no device access)."""
+    a = _lib.PrefillArgs()
+    a.q = r.q.data_ptr()
+    a.k = r.k.data_ptr()
+    a.v = r.v.data_ptr()
+    a.o = out.data_ptr()
+    a.lse = lse.data_ptr() if lse is not None else None
+    a.q_stride[:] = _batch_strides(r.q, r.B, "q")
+    a.k_stride[:] = _batch_strides(r.k, r.B, "k")
+    a.v_stride[:] = _batch_strides(r.v, r.B, "v")
+    a.o_stride[:] = list(out.stride())
+    if lse is not None:
+        a.lse_stride[:] = list(lse.stride()[:3])
+    a.batch = r.B
+    a.heads_q = r.H_q
+    a.heads_kv = r.H_kv
+    a.seqlen_q = r.S_q
+    a.seqlen_kv = r.S_kv
+    a.head_dim = r.D
+    a.q_offset = r.q_offset
+    a.causal = 1 if r.causal else 0
+    a.window = r.sliding_window if r.sliding_window is not None else 0
+    a.scale = r.scale
+    a.softcap = r.softcap if r.softcap is not None else 0.0
+    a.ref_block_q = r.block_q
+    a.ref_block_kv = r.block_kv
+    a.masked_lse_mode = 1 if r.two_pass else 0
+    a.dtype = dtype_code
+    return a
+
+
+def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> PrefillCall:
+    """Resolve arguments, check device/dtype/features, allocate outputs, build the ABI
+    struct. Launches nothing."""
+    r = resolve_forward_args(*args, **kwargs)
+    if r.block_mask is not None:
+        raise NotImplementedError(
+            "fastest_flash_attention_amd: block_mask is not supported by the HIP kernel yet"
+        )
+    if r.compute_dtype is not None and r.compute_dtype != r.q.dtype:
+        raise NotImplementedError(
+            "fastest_flash_attention_amd: compute_dtype different from the input dtype is "
+            "not supported by the HIP kernel yet"
+        )
+    for name, t in (("q", r.q), ("k", r.k), ("v", r.v)):
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"fastest_flash_attention_amd runs on ROCm GPU tensors only; {name} is on "
+                f"{t.device} (there is no CPU path)"
+            )
+    if not (r.q.device == r.k.device == r.v.device):
+        raise RuntimeError("q, k, v must be on the same device")
+    if not (r.q.dtype == r.k.dtype == r.v.dtype):
+        raise TypeError(f"q/k/v dtypes differ: {r.q.dtype}, {r.k.dtype}, {r.v.dtype}")
+    code = _lib.dtype_code(r.q.dtype)
+    if r.D > 256:
+        raise ValueError(f"head_dim {r.D} > 256 is not supported")
+    r.q = _unit_last(r.q)
+    r.k = _unit_last(r.k)
+    r.v = _unit_last(r.v)
+    if out is None:
+        out = torch.empty((r.B, r.H_q, r.S_q, r.D), dtype=r.q.dtype, device=r.q.device)
+    lse = (
+        torch.empty((r.B, r.H_q, r.S_q, 1), dtype=torch.float32, device=r.q.device)
+        if r.return_lse
+        else None
+    )
+    return PrefillCall(build_prefill_args(r, out, lse, code), r.q, r.k, r.v, out, lse, r.squeezed)
+
+
+def launch_prefill(call: PrefillCall) -> None:
+    lib = _lib.load()
+    stream = _lib.current_stream_handle(call.q.device)
+    with torch.cuda.device(call.q.device):
+        rc = lib.ffa_prefill_fwd(ctypes.byref(call.args), ctypes.c_void_p(stream))
+    _lib.check(rc)
+
+
+def fastest_flash_attn_forward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    config: Optional[AttentionConfig] = None,
+    *,
+    scale: Optional[float] = None,
+    causal: bool = False,
+    block_size: Optional[int] = None,
+    block_mask: Optional[torch.Tensor] = None,
+    softcap: Optional[float] = None,
+    sliding_window: Optional[int] = None,
+    two_pass: bool = False,
+    compute_dtype: Optional[torch.dtype] = None,
+    num_kv_heads: Optional[int] = None,
+    kv_cache: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+    return_lse: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Forward attention on MI355X. Same signature and results as the reference's
+    ``fastest_flash_attn_forward`` (ops/attention_forward.py:23-167).
+
+    Returns ``(output, lse_or_None)``: output has q's shape and dtype; lse is fp32
+    ``[B, H, S_q, 1]`` (``[B, S_q, 1]`` for 3D input), natural log.
+    """
+    call = prepare_prefill(
+        q, k, v, config,
+        scale=scale, causal=causal, block_size=block_size, block_mask=block_mask,
+        softcap=softcap, sliding_window=sliding_window, two_pass=two_pass,
+        compute_dtype=compute_dtype, num_kv_heads=num_kv_heads, kv_cache=kv_cache,
+        return_lse=return_lse,
+    )
+    launch_prefill(call)
+    output, lse = call.out, call.lse
+    if call.squeezed:
+        output = output.squeeze(1)
+        if lse is not None:
+            lse = lse.squeeze(1)
+    return output, lse

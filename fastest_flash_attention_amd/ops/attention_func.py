@@ -1,0 +1,61 @@
+"""Autograd wrapper around the HIP forward (reference ops/attention_func.py:20-125).
+
+The forward is ``fastest_flash_attn_forward`` with ``return_lse=True`` (the reference
+saves q, k, v, O, LSE for a recompute backward). The backward pass is not part of
+this build: calling it raises NotImplementedError instead of silently routing through
+another implementation.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch.autograd import Function
+
+from .attention_forward import fastest_flash_attn_forward
+
+
+class FastestFlashAttnFunc(Function):
+    @staticmethod
+    def forward(ctx, q, k, v, scale, causal, block_size, softcap, sliding_window, two_pass,
+                num_kv_heads=None):
+        output, lse = fastest_flash_attn_forward(
+            q, k, v,
+            scale=scale, causal=causal, block_size=block_size, softcap=softcap,
+            sliding_window=sliding_window, two_pass=two_pass, num_kv_heads=num_kv_heads,
+            return_lse=True,
+        )
+        ctx.save_for_backward(q, k, v, output, lse)
+        ctx.scale = scale
+        ctx.causal = causal
+        ctx.block_size = block_size
+        ctx.softcap = softcap
+        ctx.sliding_window = sliding_window
+        return output
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        raise NotImplementedError(
+            "fastest_flash_attention_amd implements the forward pass only; the attention "
+            "backward kernel is not part of this build"
+        )
+
+
+def fastest_flash_attn_func(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: Optional[float] = None,
+    causal: bool = False,
+    block_size: int = 64,
+    softcap: Optional[float] = None,
+    sliding_window: Optional[int] = None,
+    two_pass: bool = False,
+    num_kv_heads: Optional[int] = None,
+) -> torch.Tensor:
+    """Differentiable-API forward (reference ops/attention_func.py:93-125). The extra
+    trailing ``num_kv_heads`` lets GQA callers skip materialising repeated KV heads."""
+    return FastestFlashAttnFunc.apply(
+        q, k, v, scale, causal, block_size, softcap, sliding_window, two_pass, num_kv_heads,
+    )

@@ -1,0 +1,191 @@
+/*
+ * ffa.h — C ABI of the MI355X (gfx950) forward-attention library `libffa.so`.
+ *
+ * Plain C: pointers, sizes and one POD argument struct per entry point. No torch
+ * or HIP types cross this boundary (the stream is passed as `void*` holding a
+ * `hipStream_t`). The caller owns every buffer, including the split-K workspace
+ * of paged decode; the library allocates nothing on these paths and launches
+ * asynchronously on the given stream. Every entry point returns FFA_OK (0) or a
+ * negative ffa_status; exceptions never cross the ABI. Entry points are stateless
+ * and reentrant.
+ *
+ * Reference interfaces replaced (paths relative to MindIntels/fastest_flash_attention):
+ *   ffa_prefill_fwd        <- ffpa_attn_triton_forward   kernels/triton_ffpa.py:217-306
+ *                             flash_attn_triton_forward  kernels/triton_fwd.py:144-224
+ *                             (both reached from the GPU branch of
+ *                              ops/attention_forward.py:112-143; the CPU branch
+ *                              flash_attn_cpu_forward kernels/cpu_reference.py:132-312
+ *                              defines the semantics)
+ *   ffa_paged_gather       <- PagedKVCache.get_kv        ops/kv_cache.py:208-232
+ *   ffa_paged_decode_fwd   <- PagedKVCache.get_kv + fastest_flash_attn_forward(S_q=1)
+ *                             ops/kv_cache.py:208-232, ops/attention_forward.py:23-167
+ *   ffa_paged_decode_workspace_bytes, ffa_paged_decode_num_splits: sizing helpers of
+ *                             the decode entry point (no reference counterpart; the
+ *                             reference has no fused decode).
+ *   ffa_strerror, ffa_abi_version: error text / version probe, replacing the
+ *                             availability probe check_triton_available utils.py:20-29.
+ */
+#ifndef FFA_H_
+#define FFA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FFA_ABI_VERSION 1
+
+typedef enum ffa_status {
+  FFA_OK = 0,
+  FFA_ERR_INVALID_ARG = -1,      /* null pointer, non-positive size, bad stride, ... */
+  FFA_ERR_UNSUPPORTED_DTYPE = -2,
+  FFA_ERR_UNSUPPORTED_HEAD_DIM = -3,
+  FFA_ERR_MISALIGNED = -4,       /* reserved: misaligned operands take a scalar path */
+  FFA_ERR_GQA_RATIO = -5,        /* heads_q not a multiple of heads_kv */
+  FFA_ERR_WORKSPACE = -6,        /* decode workspace missing or too small */
+  FFA_ERR_LAUNCH = -7,           /* hipGetLastError() reported a launch failure */
+  FFA_ERR_NO_DEVICE = -8,        /* no usable HIP device / device query failed */
+  FFA_ERR_TOO_LARGE = -9         /* a size exceeds what the kernels index with 32 bits */
+} ffa_status;
+
+typedef enum ffa_dtype {
+  FFA_DTYPE_BF16 = 0,
+  FFA_DTYPE_FP16 = 1
+} ffa_dtype;
+
+/*
+ * Prefill / general forward attention.
+ *
+ * Semantics (kernels/cpu_reference.py:132-312, ops/attention_forward.py:23-167):
+ *   S      = (q . k^T) * scale                       fp32 accumulation
+ *   S      = softcap * tanh(S / softcap)              if softcap > 0, before masking
+ *   masked : key >= seqlen_kv,
+ *            causal && key > q_offset + row,          (top-left aligned when q_offset=0)
+ *            window > 0 && key < q_offset + row - window + 1   (one-sided if !causal)
+ *   O      = softmax(S) . v   (rows with no visible key: O = 0)
+ *   lse    = natural-log logsumexp of the visible S of the row, fp32.
+ *            A row with no visible key gets the reference's sentinel
+ *            log(n * 1e-30), n = number of (ref_block_q x ref_block_kv) tiles the
+ *            reference loop visits for that row (-inf when n == 0, and always -inf
+ *            with masked_lse_mode = 1).
+ * GQA: q head h reads kv head h / (heads_q / heads_kv)  (utils.py:111-130).
+ * Layout: element strides per tensor in order [batch, head, seq, dim]; the dim
+ * stride must be 1. A batch or head stride may be 0 (broadcast). lse strides are
+ * [batch, head, seq]. q/k/v/o share the dtype.
+ */
+typedef struct ffa_prefill_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;               /* NULL: do not write LSE */
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t o_stride[4];
+  int64_t lse_stride[3];
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t seqlen_q;
+  int32_t seqlen_kv;
+  int32_t head_dim;         /* 1..256 */
+  int32_t q_offset;         /* absolute position of query row 0 */
+  int32_t causal;           /* 0 / 1 */
+  int32_t window;           /* <= 0: no sliding window */
+  float scale;
+  float softcap;            /* <= 0: no softcap */
+  int32_t ref_block_q;      /* reference tile sizes: only used for the LSE sentinel */
+  int32_t ref_block_kv;     /*   of rows with no visible key; <= 0 means 64 */
+  int32_t masked_lse_mode;  /* 0: one-pass sentinel log(n*1e-30); 1: -inf (the
+                               reference's two_pass LSE, cpu_reference.py:63-125) */
+  int32_t dtype;            /* ffa_dtype */
+} ffa_prefill_args;
+
+int ffa_prefill_fwd(const ffa_prefill_args* args, void* stream);
+
+/*
+ * Paged KV pool, layout of PagedKVCache (ops/kv_cache.py:142-149):
+ *   k_pages, v_pages : [num_pages, heads_kv, page_size, head_dim], contiguous.
+ * Index law (ops/kv_cache.py:194-203): token t of sequence b lives in physical
+ * page block_tables[b * block_table_stride + t / page_size], slot t % page_size.
+ */
+
+/* Gather sequence pages into contiguous [heads_kv, context_len, head_dim] (get_kv). */
+typedef struct ffa_paged_gather_args {
+  const void* k_pages;
+  const void* v_pages;
+  void* k_out;              /* [heads_kv, context_len, head_dim] contiguous */
+  void* v_out;
+  const int32_t* page_table;/* device, >= ceil(context_len / page_size) entries */
+  int32_t num_pages;        /* pool size, for bounds of page ids */
+  int32_t heads_kv;
+  int32_t page_size;
+  int32_t head_dim;
+  int32_t context_len;
+  int32_t elem_bytes;       /* 2 or 4 */
+} ffa_paged_gather_args;
+
+int ffa_paged_gather(const ffa_paged_gather_args* args, void* stream);
+
+/*
+ * Batched paged decode: one query token per sequence, attending to the first
+ * context_lens[b] tokens of sequence b. The query sits at absolute position
+ * context_lens[b]-1, i.e. the reference call
+ *   fastest_flash_attn_forward(q[b:b+1,:,None], K, V, num_kv_heads=Hkv,
+ *                              kv_cache=(K[:, :, :L-1], V[:, :, :L-1]) ...)
+ * with K, V = get_kv(seq b): every cached key is visible, a sliding window keeps
+ * keys >= L - window, softcap as in prefill.
+ *   q   : [batch, heads_q, head_dim] (strides q_stride[b, h], dim stride 1)
+ *   o   : [batch, heads_q, head_dim] (strides o_stride[b, h])
+ *   lse : [batch, heads_q] fp32 (strides lse_stride[b, h]) or NULL
+ * context_lens[b] == 0 gives O = 0 and lse = -inf.
+ * Split-K: each sequence is cut into chunks of tokens_per_split tokens processed
+ * by independent workgroups; partials (O, lse) go to the caller's workspace and
+ * are merged by logsumexp weights.
+ */
+typedef struct ffa_paged_decode_args {
+  const void* q;
+  const void* k_pages;
+  const void* v_pages;
+  void* o;
+  float* lse;
+  const int32_t* block_tables;   /* [batch, block_table_stride] int32 */
+  const int32_t* context_lens;   /* [batch] int32 */
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t q_stride[2];
+  int64_t o_stride[2];
+  int64_t lse_stride[2];
+  int32_t block_table_stride;
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t head_dim;              /* 1..256 */
+  int32_t page_size;
+  int32_t num_pages;
+  int32_t max_context_len;       /* upper bound of context_lens (sizes the grid) */
+  int32_t tokens_per_split;      /* 0: library default */
+  int32_t window;                /* <= 0: none */
+  float scale;
+  float softcap;                 /* <= 0: none */
+  int32_t dtype;                 /* ffa_dtype */
+} ffa_paged_decode_args;
+
+/* Split count per sequence the decode entry point uses for these sizes. */
+int32_t ffa_paged_decode_num_splits(int32_t max_context_len, int32_t tokens_per_split);
+/* Workspace bytes needed by ffa_paged_decode_fwd for these sizes. */
+size_t ffa_paged_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
+                                        int32_t max_context_len, int32_t tokens_per_split);
+int ffa_paged_decode_fwd(const ffa_paged_decode_args* args, void* stream);
+
+const char* ffa_strerror(int status);
+int ffa_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FFA_H_ */

@@ -1,0 +1,78 @@
+"""The unchanged callers (MHA / GQA / MLA modules) on the GPU path."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import fastest_flash_attention_amd as ffa
+from fastest_flash_attention_amd.utils import repeat_kv
+from tests.gpu_util import require_gpu, say
+
+pytestmark = pytest.mark.gpu
+
+
+def test_mha_module_matches_manual_composition():
+    require_gpu()
+    torch.manual_seed(0)
+    m = ffa.FastestFlashMHA(hidden_size=256, num_heads=4, causal=True).cuda().to(torch.bfloat16)
+    m.eval()
+    x = torch.randn(2, 77, 256, device="cuda").to(torch.bfloat16)
+    say("module MHA")
+    out, lse = m(x, return_lse=True)
+    q = m.q_proj(x).view(2, 77, 4, 64).transpose(1, 2)
+    k = m.k_proj(x).view(2, 77, 4, 64).transpose(1, 2)
+    v = m.v_proj(x).view(2, 77, 4, 64).transpose(1, 2)
+    a, l2 = ffa.fastest_flash_attn_forward(q.contiguous(), k.contiguous(), v.contiguous(),
+                                           causal=True, return_lse=True)
+    ref = m.o_proj(a.transpose(1, 2).reshape(2, 77, 256))
+    assert torch.equal(out, ref) and torch.equal(lse, l2)
+
+
+def test_gqa_module_index_map_equals_repeat_kv():
+    """The module passes unrepeated KV heads; the result must equal the reference's
+    materialised repeat_kv path bit for bit."""
+    require_gpu()
+    torch.manual_seed(1)
+    m = ffa.FastestFlashGQA(hidden_size=256, num_heads=8, num_kv_heads=2, causal=True,
+                            softcap=30.0, sliding_window=40).cuda().to(torch.bfloat16)
+    m.eval()
+    x = torch.randn(2, 90, 256, device="cuda").to(torch.bfloat16)
+    say("module GQA")
+    out = m(x)
+    q = m.q_proj(x).view(2, 90, 8, 32).transpose(1, 2)
+    k = repeat_kv(m.k_proj(x).view(2, 90, 2, 32).transpose(1, 2), 8, 2)
+    v = repeat_kv(m.v_proj(x).view(2, 90, 2, 32).transpose(1, 2), 8, 2)
+    a, _ = ffa.fastest_flash_attn_forward(q, k, v, causal=True, softcap=30.0,
+                                          sliding_window=40)
+    ref = m.o_proj(a.transpose(1, 2).reshape(2, 90, 256))
+    assert torch.equal(out, ref)
+
+
+def test_mla_module_d192():
+    require_gpu()
+    torch.manual_seed(2)
+    m = ffa.FastestFlashMLA(hidden_size=512, num_heads=4, head_dim=128, latent_dim=64,
+                            rope_dim=64).cuda().to(torch.bfloat16)
+    m.eval()
+    x = torch.randn(1, 130, 512, device="cuda").to(torch.bfloat16)
+    say("module MLA")
+    out = m(x)
+    q, k, vp = m.project_qkv(x)
+    assert q.shape[-1] == 192 and q.dtype == torch.bfloat16
+    a, _ = ffa.fastest_flash_attn_forward(q, k, vp, scale=m.scale, causal=True)
+    assert torch.equal(out, m.o_proj(a.transpose(1, 2).reshape(1, 130, -1)))
+    assert torch.isfinite(out).all()
+
+
+def test_training_mode_forward_and_backward_contract():
+    require_gpu()
+    torch.manual_seed(3)
+    m = ffa.FastestFlashMHA(hidden_size=128, num_heads=2, causal=True).cuda().to(torch.bfloat16)
+    m.train()
+    x = torch.randn(1, 40, 128, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    say("module training-mode forward")
+    out = m(x)
+    assert out.shape == (1, 40, 128)
+    with pytest.raises(NotImplementedError):
+        out.float().sum().backward()

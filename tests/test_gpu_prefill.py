@@ -1,0 +1,201 @@
+"""GPU parity of the prefill kernel (ffa_prefill_fwd through fastest_flash_attn_forward)
+against the CPU oracle (oracle/reference_forward.py) on identical seeded inputs."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fastest_flash_attention_amd as ffa
+from oracle import reference_forward as rf
+from tests.gpu_util import assert_parity, np32, require_gpu, say, seeded
+
+pytestmark = pytest.mark.gpu
+
+BF16, F16 = torch.bfloat16, torch.float16
+
+# (name, B, Hq, Hkv, Sq, Skv, D, kwargs, dtype)
+CASES = [
+    ("plain", 2, 4, 4, 128, 128, 64, {}, BF16),
+    ("causal_tail", 1, 3, 3, 200, 200, 128, {"causal": True}, BF16),
+    ("causal_window", 1, 2, 2, 300, 300, 128, {"causal": True, "sliding_window": 37}, BF16),
+    ("softcap_causal", 2, 2, 2, 150, 150, 64, {"causal": True, "softcap": 10.0}, BF16),
+    ("gqa", 1, 8, 2, 256, 256, 128, {"causal": True, "num_kv_heads": 2}, BF16),
+    ("mqa_broadcast", 1, 4, 1, 96, 96, 64, {}, BF16),
+    ("d192_mla", 1, 2, 2, 256, 256, 192, {"causal": True}, BF16),
+    ("d256", 1, 2, 2, 130, 130, 256, {"causal": True}, BF16),
+    ("d96", 1, 2, 2, 77, 77, 96, {"causal": True}, BF16),
+    ("d16", 2, 2, 2, 40, 40, 16, {}, BF16),
+    ("d8_scalar", 1, 2, 2, 17, 17, 8, {"causal": True}, BF16),
+    ("d4_scalar", 1, 1, 1, 8, 8, 4, {}, BF16),
+    ("fp16", 1, 4, 4, 200, 200, 128, {"causal": True, "softcap": 30.0}, F16),
+    ("sq_ne_skv", 1, 2, 2, 64, 300, 64, {}, BF16),
+    ("causal_sq_lt_skv", 1, 2, 2, 64, 300, 64, {"causal": True}, BF16),
+    ("window_noncausal_masked_rows", 1, 2, 2, 32, 8, 16, {"sliding_window": 4,
+                                                          "block_size": 4}, BF16),
+    ("single", 1, 2, 2, 1, 1, 64, {}, BF16),
+    ("gqa_window_softcap", 2, 8, 2, 333, 333, 128, {"causal": True, "sliding_window": 100,
+                                                    "softcap": 50.0, "num_kv_heads": 2}, BF16),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_prefill_parity(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, D, kw, dt = case
+    q = seeded((B, Hq, Sq, D), dt, 1)
+    k = seeded((B, Hkv, Skv, D), dt, 2)
+    v = seeded((B, Hkv, Skv, D), dt, 3)
+    say(f"prefill {name} B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} {kw} {dt}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), return_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert o.dtype == dt and o.shape == q.shape and lse.shape == (B, Hq, Sq, 1)
+    ro, rl = rf.forward(np32(q), np32(k), np32(v), return_lse=True, **kw)
+    assert_parity(o, ro, lse, rl, name)
+
+
+def test_kv_cache_offset():
+    require_gpu()
+    B, H, D = 2, 4, 128
+    q = seeded((B, H, 70, D), BF16, 4)
+    kn = seeded((B, H, 70, D), BF16, 5)
+    vn = seeded((B, H, 70, D), BF16, 6)
+    kc = seeded((B, H, 200, D), BF16, 7)
+    vc = seeded((B, H, 200, D), BF16, 8)
+    for causal in (False, True):
+        say(f"prefill kv_cache causal={causal}")
+        o, lse = ffa.fastest_flash_attn_forward(q.cuda(), kn.cuda(), vn.cuda(), causal=causal,
+                                                kv_cache=(kc.cuda(), vc.cuda()),
+                                                return_lse=True)
+        ro, rl = rf.forward(np32(q), np32(kn), np32(vn), causal=causal,
+                            kv_cache=(np32(kc), np32(vc)), return_lse=True)
+        assert_parity(o, ro, lse, rl, f"kv_cache causal={causal}")
+
+
+def test_negative_offset_masked_rows():
+    """q longer than the concatenated keys: q_offset < 0, early causal rows see no key
+    and must carry the reference sentinel LSE."""
+    require_gpu()
+    q = seeded((1, 2, 40, 64), BF16, 9)
+    kn = seeded((1, 2, 6, 64), BF16, 10)
+    kc = seeded((1, 2, 10, 64), BF16, 11)
+    say("prefill negative q_offset")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), kn.cuda(), kn.cuda(), causal=True,
+                                            kv_cache=(kc.cuda(), kc.cuda()), block_size=8,
+                                            return_lse=True)
+    ro, rl = rf.forward(np32(q), np32(kn), np32(kn), causal=True, kv_cache=(np32(kc), np32(kc)),
+                        block_size=8, return_lse=True)
+    assert np.isneginf(rl).any() or (rl < -60).any()
+    assert_parity(o, ro, lse, rl, "negative offset")
+
+
+def test_two_pass_sentinel():
+    require_gpu()
+    q = seeded((1, 2, 32, 16), BF16, 12)
+    k = seeded((1, 2, 8, 16), BF16, 13)
+    say("prefill two_pass masked rows")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), k.cuda(), sliding_window=4,
+                                            block_size=4, two_pass=True, return_lse=True)
+    _, rl = rf.forward(np32(q), np32(k), np32(k), sliding_window=4, block_size=4,
+                       two_pass=True, return_lse=True)
+    lse_c = np32(lse)
+    assert np.array_equal(np.isneginf(lse_c), np.isneginf(rl))
+    assert np.all(np32(o)[0, :, 11:] == 0)
+
+
+def test_module_layout_views_and_3d():
+    """Strided [B,H,S,D] views of [B,S,H*D] projections (the modules' layout) and 3D input."""
+    require_gpu()
+    B, S, H, D = 2, 100, 4, 64
+    x = seeded((B, S, 3 * H * D), BF16, 14).cuda()
+    q, k, v = (t.view(B, S, H, D).transpose(1, 2) for t in x.split(H * D, dim=-1))
+    say("prefill strided views")
+    o, lse = ffa.fastest_flash_attn_forward(q, k, v, causal=True, return_lse=True)
+    ro, rl = rf.forward(np32(q), np32(k), np32(v), causal=True, return_lse=True)
+    assert_parity(o, ro, lse, rl, "strided views")
+    q3 = seeded((3, 50, 32), BF16, 15)
+    say("prefill 3d")
+    o3, l3 = ffa.fastest_flash_attn_forward(q3.cuda(), q3.cuda(), q3.cuda(), causal=True,
+                                            return_lse=True)
+    assert o3.shape == (3, 50, 32) and l3.shape == (3, 50, 1)
+    ro3, rl3 = rf.forward(np32(q3), np32(q3), np32(q3), causal=True, return_lse=True)
+    assert_parity(o3, ro3, l3, rl3, "3d")
+
+
+def test_batch_broadcast_kv():
+    require_gpu()
+    q = seeded((3, 2, 64, 64), BF16, 16)
+    k = seeded((1, 2, 64, 64), BF16, 17)
+    say("prefill batch-broadcast kv")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), k.cuda(), return_lse=True)
+    ro, rl = rf.forward(np32(q), np32(k), np32(k), return_lse=True)
+    assert_parity(o, ro, lse, rl, "batch broadcast")
+
+
+def test_special_values():
+    """Closed forms on the device: one key -> O = V; zero q -> mean(V)."""
+    require_gpu()
+    v = seeded((1, 2, 1, 64), BF16, 18)
+    q = seeded((1, 2, 9, 64), BF16, 19)
+    o, _ = ffa.fastest_flash_attn_forward(q.cuda(), v.cuda(), v.cuda())
+    assert torch.equal(o.cpu(), v.expand_as(o))
+    qz = torch.zeros(1, 1, 16, 64, dtype=BF16)
+    kv = seeded((1, 1, 48, 64), BF16, 20)
+    o, _ = ffa.fastest_flash_attn_forward(qz.cuda(), kv.cuda(), kv.cuda())
+    assert np.abs(np32(o) - np32(kv).mean(axis=2, keepdims=True)).max() < 1e-2
+
+
+def test_rejects_unsupported():
+    require_gpu()
+    q = torch.randn(1, 1, 8, 16, device="cuda")
+    with pytest.raises(TypeError):
+        ffa.fastest_flash_attn_forward(q, q, q)
+    qb = q.to(BF16)
+    with pytest.raises(NotImplementedError):
+        ffa.fastest_flash_attn_forward(qb, qb, qb, block_mask=torch.ones(1, 1, dtype=torch.bool))
+
+
+# ---------------------------------------------------------------------------------
+# BASELINE configs at full size: the kernel runs the whole batch, the oracle checks
+# sampled (batch, head) pairs exactly (rows are independent), plus global invariants.
+# ---------------------------------------------------------------------------------
+
+FULL = [
+    ("cfg2_mha", 4, 32, 32, 4096, 128, {"causal": True}, [(0, 0), (3, 31)]),
+    ("north_star", 4, 32, 32, 8192, 128, {"causal": True}, [(1, 5)]),
+    ("cfg3_gqa", 2, 32, 8, 8192, 128, {"causal": True, "sliding_window": 4096,
+                                        "softcap": 50.0, "num_kv_heads": 8}, [(0, 0), (1, 31)]),
+    ("cfg5_mla_d192", 2, 32, 32, 4096, 192, {"causal": True}, [(1, 17)]),
+]
+
+
+@pytest.mark.parametrize("cfg", FULL, ids=[c[0] for c in FULL])
+def test_full_size_sampled_heads(cfg):
+    require_gpu()
+    name, B, Hq, Hkv, S, D, kw, samples = cfg
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(B, Hq, S, D, generator=g, device="cuda").to(BF16)
+    k = torch.randn(B, Hkv, S, D, generator=g, device="cuda").to(BF16)
+    v = torch.randn(B, Hkv, S, D, generator=g, device="cuda").to(BF16)
+    say(f"prefill full {name}")
+    o, lse = ffa.fastest_flash_attn_forward(q, k, v, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    ratio = Hq // Hkv
+    okw = {kk: vv for kk, vv in kw.items() if kk != "num_kv_heads"}
+    for b, h in samples:
+        hk = h // ratio
+        ro, rl = rf.flash_attn_cpu_forward(
+            np32(q[b:b + 1, h:h + 1]), np32(k[b:b + 1, hk:hk + 1]), np32(v[b:b + 1, hk:hk + 1]),
+            scale=1 / math.sqrt(D), block_q=256, block_kv=256, return_lse=True,
+            causal=okw.get("causal", False), sliding_window=okw.get("sliding_window"),
+            softcap=okw.get("softcap"))
+        assert_parity(o[b:b + 1, h:h + 1], ro, lse[b:b + 1, h:h + 1], rl, f"{name} b{b} h{h}")
+    # size-independent property: LSE >= max visible score and the first row attends only
+    # to key 0 under causal masking -> O[:, :, 0] == V[:, kv(h), 0]
+    o0 = o[:, :, 0].float()
+    v0 = v[:, torch.arange(Hq, device="cuda") // ratio, 0].float()
+    assert (o0 - v0).abs().max().item() < 1e-2

@@ -1,0 +1,242 @@
+"""Host-side tests (no GPU): argument resolution of the drop-in boundary, the C ABI
+(struct layout against the header compiled by gcc, exported symbols, validation
+error codes), and PagedKVCache bookkeeping against the oracle's restatement."""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import re
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+import torch
+
+import fastest_flash_attention_amd as ffa
+from fastest_flash_attention_amd.kernels import _lib
+from fastest_flash_attention_amd.ops import attention_forward as af
+from oracle import paged as opaged
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "ffa.h")
+
+
+@pytest.fixture(scope="session")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from fastest_flash_attention_amd.kernels.hip import build
+
+        build.build(verbose=False)
+    return _lib.load()
+
+
+# ---------------------------------------------------------------------------------
+# Argument resolution (reference ops/attention_forward.py:65-109)
+# ---------------------------------------------------------------------------------
+
+def test_config_overrides_kwargs():
+    q = torch.randn(2, 2, 16, 8)
+    cfg = ffa.AttentionConfig(causal=True, softcap=3.0, sliding_window=5, return_lse=True,
+                              block_size_q=4, block_size_kv=8)
+    r = af.resolve_forward_args(q, q, q, cfg, causal=False, softcap=None, return_lse=False)
+    assert r.causal and r.softcap == 3.0 and r.sliding_window == 5 and r.return_lse
+    assert (r.block_q, r.block_kv) == (4, 8)
+    r = af.resolve_forward_args(q, q, q, cfg, block_size=16)
+    assert (r.block_q, r.block_kv) == (16, 16)  # explicit block_size beats config
+
+
+def test_auto_block_size_and_scale():
+    q = torch.randn(1, 2, 4096, 128)
+    r = af.resolve_forward_args(q, q, q)
+    assert r.block_q == r.block_kv == 32 and math.isclose(r.scale, 1 / math.sqrt(128))
+    assert ffa.auto_select_block_size(1024, 1024, 64) == 64
+    assert ffa.auto_select_block_size(4096, 4096, 192) == 16
+
+
+def test_kv_cache_offset_and_3d():
+    q = torch.randn(2, 5, 8)
+    kc = torch.randn(2, 7, 8)
+    r = af.resolve_forward_args(q, q, q, kv_cache=(kc, kc))
+    assert r.squeezed and r.q.shape == (2, 1, 5, 8)
+    assert r.S_kv == 12 and r.q_offset == 7
+
+
+def test_gqa_rules():
+    q = torch.randn(1, 8, 4, 16)
+    k = torch.randn(1, 2, 4, 16)
+    r = af.resolve_forward_args(q, k, k, num_kv_heads=2)
+    assert (r.H_q, r.H_kv) == (8, 2)
+    with pytest.raises(ValueError, match="num_kv_heads"):
+        af.resolve_forward_args(q, k, k)
+    k1 = torch.randn(1, 1, 4, 16)  # MQA broadcasts without num_kv_heads, as torch.matmul does
+    assert af.resolve_forward_args(q, k1, k1).H_kv == 1
+    with pytest.raises(ValueError):
+        af.resolve_forward_args(q, torch.randn(1, 3, 4, 16), torch.randn(1, 3, 4, 16),
+                                num_kv_heads=3)
+
+
+def test_build_args_strides_of_module_views():
+    B, S, H, D = 2, 10, 4, 16
+    x = torch.randn(B, S, H * D)
+    q = x.view(B, S, H, D).transpose(1, 2)  # the modules' strided view
+    k = torch.randn(1, H, S, D)              # batch-broadcast K
+    r = af.resolve_forward_args(q, k, k, causal=True, sliding_window=3, softcap=2.0,
+                                two_pass=True, block_size=8)
+    out = torch.empty(B, H, S, D)
+    lse = torch.empty(B, H, S, 1)
+    a = af.build_prefill_args(r, out, lse, _lib.FFA_DTYPE_BF16)
+    assert list(a.q_stride) == [S * H * D, D, H * D, 1]
+    assert list(a.k_stride) == [0, S * D, D, 1]
+    assert list(a.lse_stride) == [H * S, S, 1]
+    assert (a.causal, a.window, a.softcap, a.masked_lse_mode) == (1, 3, 2.0, 1)
+    assert (a.ref_block_q, a.ref_block_kv, a.q_offset) == (8, 8, 0)
+    assert a.q == q.data_ptr() and a.o == out.data_ptr()
+
+
+def test_product_path_refuses_cpu_and_unsupported():
+    q = torch.randn(1, 1, 8, 16, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
+        ffa.fastest_flash_attn_forward(q, q, q)
+    with pytest.raises(NotImplementedError):
+        af.prepare_prefill(q, q, q, block_mask=torch.ones(1, 1, dtype=torch.bool))
+    cache = ffa.PagedKVCache(max_pages=4, page_size=4, num_heads=1, head_dim=8)
+    cache.append_tokens(0, torch.randn(1, 3, 8), torch.randn(1, 3, 8))
+    with pytest.raises(RuntimeError, match="ROCm"):
+        cache.get_kv(0)
+
+
+# ---------------------------------------------------------------------------------
+# C ABI
+# ---------------------------------------------------------------------------------
+
+def _header_functions() -> list[str]:
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(ffa_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_header_symbol(lib):
+    names = _header_functions()
+    assert set(names) == set(_lib.EXPORTS), names
+    for name in names:
+        assert hasattr(lib, name)
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    for name in names:
+        assert re.search(rf"\bT {name}$", out, re.M), name
+
+
+def _c_layout(struct: str, fields: list[str]) -> dict:
+    src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(){"]
+    src.append(f'printf("sizeof %zu\\n", sizeof({struct}));')
+    for f in fields:
+        src.append(f'printf("{f} %zu\\n", offsetof({struct}, {f}));')
+    src.append("return 0;}")
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "l.c")
+        exe = os.path.join(d, "l")
+        open(c, "w").write("\n".join(src))
+        subprocess.run(["gcc", "-std=c11", c, "-o", exe], check=True)
+        text = subprocess.run([exe], capture_output=True, text=True, check=True).stdout
+    return {k: int(v) for k, v in (ln.split() for ln in text.splitlines())}
+
+
+@pytest.mark.parametrize("cls,cname", [
+    (_lib.PrefillArgs, "ffa_prefill_args"),
+    (_lib.PagedGatherArgs, "ffa_paged_gather_args"),
+    (_lib.PagedDecodeArgs, "ffa_paged_decode_args"),
+])
+def test_ctypes_struct_matches_header(cls, cname):
+    fields = [f for f, _ in cls._fields_]
+    c = _c_layout(cname, fields)
+    assert c["sizeof"] == ctypes.sizeof(cls)
+    for f in fields:
+        assert c[f] == getattr(cls, f).offset, f
+
+
+def test_abi_version_and_strerror(lib):
+    assert lib.ffa_abi_version() == _lib.FFA_ABI_VERSION
+    for rc in range(0, -10, -1):
+        assert lib.ffa_strerror(rc).decode().strip()
+    assert b"unknown" in lib.ffa_strerror(-99)
+
+
+def test_validation_errors_without_device(lib):
+    a = _lib.PrefillArgs()
+    assert lib.ffa_prefill_fwd(None, None) == -1
+    a.dtype, a.head_dim, a.batch, a.heads_q, a.heads_kv = 0, 0, 1, 1, 1
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -3
+    a.head_dim, a.dtype = 64, 7
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -2
+    a.dtype, a.heads_q, a.heads_kv = 0, 3, 2
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -5
+    a.heads_q, a.heads_kv, a.batch, a.seqlen_q = 2, 2, 0, 4
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == 0  # empty: nothing launched
+    a.batch = 1
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -1  # null pointers
+    d = _lib.PagedDecodeArgs()
+    d.dtype, d.head_dim, d.batch, d.heads_q, d.heads_kv, d.page_size = 0, 128, 2, 8, 2, 16
+    d.max_context_len, d.block_table_stride = 64, 4
+    d.q = d.o = d.k_pages = d.v_pages = d.block_tables = d.context_lens = 16
+    d.workspace, d.workspace_bytes = 16, 8
+    assert lib.ffa_paged_decode_fwd(ctypes.byref(d), None) == -6
+    d.block_table_stride = 3
+    assert lib.ffa_paged_decode_fwd(ctypes.byref(d), None) == -1
+    g = _lib.PagedGatherArgs()
+    g.elem_bytes = 3
+    assert lib.ffa_paged_gather(ctypes.byref(g), None) == -2
+
+
+def test_workspace_sizing(lib):
+    # [B][Hq][splits][Dpad] O partials + [B][Hq][splits] lse, fp32
+    assert lib.ffa_paged_decode_num_splits(32768, 512) == 64
+    assert lib.ffa_paged_decode_num_splits(1000, 0) == 2  # default split 512
+    assert lib.ffa_paged_decode_workspace_bytes(64, 32, 128, 32768, 512) == 64 * 32 * 64 * 129 * 4
+    assert lib.ffa_paged_decode_workspace_bytes(2, 4, 100, 100, 64) == 2 * 4 * 2 * 129 * 4
+
+
+# ---------------------------------------------------------------------------------
+# PagedKVCache bookkeeping (write path) vs the oracle restatement
+# ---------------------------------------------------------------------------------
+
+def test_paged_cache_matches_oracle_bookkeeping():
+    gen = torch.Generator().manual_seed(0)
+    cache = ffa.PagedKVCache(max_pages=12, page_size=4, num_heads=2, head_dim=8,
+                             dtype=torch.float32)
+    pool = opaged.PagedPool(max_pages=12, page_size=4, num_heads=2, head_dim=8)
+    ops = [("a", 0, 6), ("a", 1, 3), ("a", 0, 5), ("f", 1, 0), ("a", 2, 9), ("a", 0, 1),
+           ("a", 2, 0)]
+    for op, sid, n in ops:
+        if op == "a":
+            k = torch.randn(2, n, 8, generator=gen)
+            v = torch.randn(2, n, 8, generator=gen)
+            assert cache.append_tokens(sid, k, v) == pool.append_tokens(sid, k.numpy(),
+                                                                      v.numpy())
+        else:
+            cache.free_sequence(sid)
+            pool.free_sequence(sid)
+        assert cache.free_pages == pool.free_pages
+        assert cache.sequences == pool.sequences
+    assert np.array_equal(cache.k_pages.numpy(), pool.k_pages)
+    assert np.array_equal(cache.v_pages.numpy(), pool.v_pages)
+    assert cache.num_free_pages == len(pool.free_pages)
+    assert cache.total_capacity == 48
+    bt, lens = cache.block_tables([2, 0, 7])
+    assert lens.tolist() == [9, 12, 0]
+    assert bt.dtype == torch.int32 and bt.shape == (3, 3)
+    assert bt[0].tolist() == pool.sequences[2]["page_table"]
+
+
+def test_paged_cache_out_of_pages_matches_reference_state():
+    cache = ffa.PagedKVCache(max_pages=1, page_size=4, num_heads=1, head_dim=2,
+                             dtype=torch.float32)
+    pool = opaged.PagedPool(max_pages=1, page_size=4, num_heads=1, head_dim=2)
+    k = torch.arange(10, dtype=torch.float32).view(1, 5, 2)
+    with pytest.raises(RuntimeError, match="out of physical pages"):
+        cache.append_tokens(0, k, k)
+    with pytest.raises(RuntimeError, match="out of physical pages"):
+        pool.append_tokens(0, k.numpy(), k.numpy())
+    assert cache.sequences == pool.sequences and cache.free_pages == pool.free_pages
+    assert np.array_equal(cache.k_pages.numpy(), pool.k_pages)
