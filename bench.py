@@ -88,50 +88,37 @@ def blas_threads() -> int:
 
 
 def cpu_baseline_prefill(cfg: dict, q, k, v, budget_s: float) -> dict:
-    """Oracle restatement of the reference CPU path on a row band of head (0, 0),
-    with the reference dispatcher's block size; rows are independent given q_offset."""
-    import numpy as np
-
+    """Oracle restatement of the reference CPU path (numpy, the reference dispatcher's
+    block size) over whole (batch 0, head h) slices, h = 0, 1, ... until the time
+    budget is spent; FLOPs counted exactly for the heads processed."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import reference_forward as rf
 
-    S, D = cfg["S"], cfg["D"]
+    S, D, ratio = cfg["S"], cfg["D"], cfg["Hq"] // cfg["Hkv"]
     bs = rf.auto_select_block_size(S, S, D)
-    q0 = q[0, 0].float().cpu().numpy()[None, None]
-    k0 = k[0, 0].float().cpu().numpy()[None, None]
-    v0 = v[0, 0].float().cpu().numpy()[None, None]
-
-    def run(r0, r1):
-        kv_end = r1 if cfg["causal"] else S
-        kv_lo = max(0, r0 - cfg["window"] + 1) if cfg["window"] else 0
-        kv_lo = (kv_lo // bs) * bs  # keep the reference's KV tile grid
+    pairs = n_valid_pairs_fast(S, cfg["causal"], cfg["window"])
+    secs, heads = 0.0, 0
+    while heads < cfg["Hq"] and (heads == 0 or secs < budget_s):
+        h = heads
+        qh = q[0:1, h:h + 1].float().numpy()
+        kh = k[0:1, h // ratio:h // ratio + 1].float().numpy()
+        vh = v[0:1, h // ratio:h // ratio + 1].float().numpy()
         t = time.perf_counter()
-        rf.flash_attn_cpu_forward(q0[:, :, r0:r1], k0[:, :, kv_lo:kv_end], v0[:, :, kv_lo:kv_end],
-                                  scale=1 / math.sqrt(D), causal=cfg["causal"], block_q=bs,
-                                  block_kv=bs, softcap=cfg["softcap"],
-                                  sliding_window=cfg["window"], q_offset=r0 - kv_lo)
-        return time.perf_counter() - t
-
-    mid = S // 2
-    rows = 64
-    t = run(mid, mid + rows)
-    rows = int(min(S - mid, max(rows, rows * budget_s / max(t, 1e-3))))
-    rows = max(bs, (rows // bs) * bs)
-    secs = run(mid, mid + rows)
-    pairs = 0
-    for i in range(mid, mid + rows):
-        hi = i if cfg["causal"] else S - 1
-        lo = max(0, i - cfg["window"] + 1) if cfg["window"] else 0
-        pairs += hi - lo + 1
-    flops = 4.0 * D * pairs
+        rf.flash_attn_cpu_forward(qh, kh, vh, scale=1 / math.sqrt(D), causal=cfg["causal"],
+                                  block_q=bs, block_kv=bs, softcap=cfg["softcap"],
+                                  sliding_window=cfg["window"])
+        secs += time.perf_counter() - t
+        heads += 1
+    flops = 4.0 * D * pairs * heads
     return {
         "value": flops / secs / 1e12,
         "unit": "TFLOP/s",
         "cores": blas_threads(),
         "kind": "port",
-        "sample": (f"oracle/reference_forward.flash_attn_cpu_forward (numpy fp32), batch 0 "
-                   f"head 0, query rows [{mid}, {mid + rows}) of S={S}, block {bs} as the "
-                   f"reference dispatcher picks; {secs:.1f} s, {flops:.3e} FLOP; "
+        "sample": (f"oracle/reference_forward.flash_attn_cpu_forward (numpy fp32, the "
+                   f"reference CPU algorithm) on batch 0, heads 0..{heads - 1} "
+                   f"({heads}/{cfg['B'] * cfg['Hq']} of the batch), all {S} rows, block {bs} "
+                   f"as the reference dispatcher picks; {secs:.1f} s for {flops:.3e} FLOP; "
                    f"os.cpu_count()={os.cpu_count()}"),
     }
 
