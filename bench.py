@@ -227,6 +227,9 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline sample (0 disables it)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="run one plain device copy of this many MiB first (a known-size "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU; --gpus must be 1 (the hot path "
@@ -239,6 +242,13 @@ def main() -> int:
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         return 1
     torch.cuda.set_device(0)
+    if args.calibrate_copy_mib > 0:
+        src = torch.ones(args.calibrate_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     pre = bench_prefill(args.workload, args.steps, args.warmup, args.cpu_seconds)
     dec = None if args.no_decode else bench_decode(args.steps, args.warmup)
     line = {

@@ -30,7 +30,8 @@ const char* ffa_strerror(int status) {
     case FFA_ERR_UNSUPPORTED_HEAD_DIM:
       return "ffa: unsupported head_dim (1..256 supported)";
     case FFA_ERR_MISALIGNED:
-      return "ffa: misaligned operand";
+      return "ffa: operands must be 16-byte aligned with head_dim and row/head/batch strides "
+             "multiples of 8 elements";
     case FFA_ERR_GQA_RATIO:
       return "ffa: heads_q must be a positive multiple of heads_kv";
     case FFA_ERR_WORKSPACE:
@@ -67,6 +68,23 @@ int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
     }
   }
   if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  // 16-byte vector / direct-to-LDS loads: aligned bases, head_dim and row strides in
+  // whole 16-byte chunks.
+  if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
+  const void* ptrs[4] = {a->q, a->k, a->v, a->o};
+  for (const void* ptr : ptrs) {
+    if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) return FFA_ERR_MISALIGNED;
+  }
+  const int64_t* strides[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
+  for (const int64_t* st : strides) {
+    for (int i = 0; i < 3; ++i) {
+      if (st[i] % 8 != 0) return FFA_ERR_MISALIGNED;
+    }
+  }
+  // per-tile byte offsets of K/V rows are 32-bit
+  if (a->k_stride[2] >= (int64_t{1} << 24) || a->v_stride[2] >= (int64_t{1} << 24)) {
+    return FFA_ERR_TOO_LARGE;
+  }
   // Positions are int32 inside the kernel.
   const int64_t max_pos = static_cast<int64_t>(a->q_offset) + a->seqlen_q;
   if (max_pos > 0x3fffffff || a->seqlen_kv > 0x3fffffff || a->q_offset < -0x3fffffff) {

@@ -22,6 +22,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -121,5 +122,24 @@ __device__ inline void quad_interleave(const u32x4& r0, const u32x4& r1, const u
 }
 
 __device__ inline float wave_xor32(float x) { return __shfl_xor(x, 32); }
+
+// gfx950 data-movement builtins, wrapped in __device__ functions (called from lambdas
+// inside kernels they must not appear in host-side code).
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// global_load_lds_dwordx4: this lane's 16 bytes at `src` land at lds_base + 16 * lane.
+__device__ inline void load_lds16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lanes 4k..4k+3 point at 16 contiguous
+// 16-bit elements of row k (4 each); lane i receives element i of rows 0..3.
+__device__ inline u32x2 lds_read_tr16(const uint16_t* lds_ptr) {
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)lds_ptr);
+  return __builtin_bit_cast(u32x2, v);
+}
+
+__device__ inline void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 }  // namespace ffa

@@ -5,26 +5,27 @@
 // q_offset, GQA head map h -> h / (Hq / Hkv), natural-log LSE.
 //
 // Work decomposition: one workgroup (4 waves, 256 threads) per (batch, q-head, 128-row
-// query tile); each wave owns 32 query rows for the whole KV sweep.
+// query tile); each wave owns 32 query rows for the whole KV sweep. Inputs must be
+// 16-byte aligned with head_dim % 8 == 0 (the host pads / copies otherwise).
 //
 // Per KV tile of BN keys (BN = 64 for head_dim <= 128, 32 above):
 //   S^T[key, q] = K Q^T   v_mfma_f32_32x32x16 with K (LDS) as A and Q (registers) as B,
-//                         so lane l holds 32*BN/64 scores of ONE query (l % 32): the
-//                         row max needs one lane swap (l ^ 32), the row sum none until
-//                         the epilogue.
-//   P = exp2(S*scale*log2e - m)   fp32, m updated only when it grows by more than
-//                         2^8 (deferred rescale: O and l are rescaled only then).
-//   O^T[d, q] += V^T P^T  A = V^T from LDS, B = P packed to 16 bit straight from the
-//                         S^T accumulator registers: the MFMA C layout of S^T holds,
-//                         per lane, exactly the keys the B operand of the next MFMA
-//                         needs once the PV contraction uses the matching key order.
-// V is stored in LDS as key quads ([key/4][dim][4 keys]) so each A operand of the PV
-// product is two 8-byte LDS reads, with no transpose instruction.
-// K/V tiles are double-buffered in LDS; the global loads of tile t+2 are in flight
-// while tile t is computed, so each iteration has a single barrier.
-// Causal / window tiles outside a workgroup's band are never loaded; tiles outside a
-// wave's band are loaded but skip the wave's MFMA work; element masks are evaluated
-// only on band-edge tiles.
+//                         so lane l holds BN/2 scores of ONE query (l % 32): the row max
+//                         needs one lane swap (l ^ 32), the row sum none until the end.
+//   P = exp2(S*c - m*c)   fp32 (c = scale*log2e, one FMA per score); m moves only when
+//                         the max grows by more than 2^8, so O and l are rarely rescaled.
+//   O^T[d, q] += V^T P^T  B = P packed to 16 bit straight from the S^T accumulators;
+//                         A = V^T from LDS by two ds_read_b64_tr_b16 (4 keys x 1 dim per
+//                         lane each) on the row-major V tile: the key order they produce
+//                         is the key order the S^T accumulator layout hands to P.
+// Data movement: K and V tiles go global -> LDS with global_load_lds_dwordx4 (no VGPR
+// staging), double-buffered, issued one tile ahead; the global side picks the 16-byte
+// chunk each lane fetches so the LDS image is XOR-swizzled per row, which makes the
+// K operand reads and the transposed V reads bank-conflict free. S^T of tile t+1 is
+// issued before the softmax of tile t so MFMA and VALU work overlap within a wave;
+// one barrier per tile.
+// Causal / window tiles outside a workgroup's band are never loaded; tiles past a
+// wave's causal band skip the wave's work; element masks run only on band-edge tiles.
 // Grid order: heaviest causal query tiles first, and (when the grid is a multiple of
 // 8) consecutive tiles of one head are placed on one XCD so its K/V stay in that L2.
 
@@ -57,25 +58,36 @@ struct PrefillParams {
   float cap_mul;    // softcap*log2e (softcap only)
   int ref_bq, ref_bkv;
   int masked_lse_mode;
-  int vec;
   int xcd_remap;
 };
 
 template <int DP, int BN>
 struct Shape {
-  static constexpr int KSTR = DP + 8;  // K row stride in 16-bit elements (16 B pad)
-  static constexpr int VSTR = DP * 4;  // V key-quad row stride in 16-bit elements
-  static constexpr int K_ELEMS = BN * KSTR;
-  static constexpr int V_ELEMS = (BN / 4) * VSTR;
-  static constexpr int KCHUNKS = BN * DP / 8;
-  static constexpr int KPT = (KCHUNKS + kThreads - 1) / kThreads;
-  static constexpr int VITEMS = (BN / 4) * (DP / 8);
-  static constexpr int VPT = (VITEMS + kThreads - 1) / kThreads;
+  static constexpr int CPR = DP / 8;            // 16-byte chunks per row
+  static constexpr int TILE = BN * DP;          // elements per K (or V) tile
+  static constexpr int LPT = BN * CPR / kThreads;  // direct loads per thread per tile
   static constexpr int NB = BN / 32;
   static constexpr int NC = BN / 16;
   static constexpr int KS = DP / 16;
   static constexpr int DB = DP / 32;
+  static_assert(BN * CPR % kThreads == 0, "tile must split evenly over the workgroup");
 };
+
+// Row swizzles (XOR on the 16-byte chunk index) of the K and V tiles in LDS. They make
+// the 16 rows read together by a K operand load, and the 4 rows x 64 bytes read
+// together by a transposed V load, land in distinct bank groups.
+template <int DP>
+__device__ inline int kswz(int r) {
+  if constexpr (DP == 32) return (r >> 2) & 3;
+  if constexpr (DP == 64 || DP == 192) return (r >> 1) & 7;
+  return r & 15;
+}
+template <int DP>
+__device__ inline int vswz(int r) {
+  if constexpr (DP == 32) return 0;
+  if constexpr (DP == 64 || DP == 192) return 4 * ((r >> 1) & 1);
+  return 4 * (r & 3);
+}
 
 // LSE of a row with no visible key, as the reference loop produces it: each visited
 // tile adds log(1e-30) by logaddexp (cpu_reference.py:288-297), so n visited tiles
@@ -115,8 +127,8 @@ template <typename Tag, int DP, int BN, bool SOFTCAP>
 __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const PrefillParams p) {
   using S = Shape<DP, BN>;
   using E = Elem<Tag>;
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][S::K_ELEMS];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][S::V_ELEMS];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][S::TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][S::TILE];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -137,9 +149,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   const int hk = h / p.ratio;
 
   const uint16_t* __restrict__ qbase = p.q + b * p.q_sb + h * p.q_sh;
-  const uint16_t* __restrict__ kbase = p.k + b * p.k_sb + hk * p.k_sh;
-  const uint16_t* __restrict__ vbase = p.v + b * p.v_sb + hk * p.v_sh;
-  const bool vec = p.vec != 0;
+  const char* kbytes = reinterpret_cast<const char*>(p.k + b * p.k_sb + hk * p.k_sh);
+  const char* vbytes = reinterpret_cast<const char*>(p.v + b * p.v_sb + hk * p.v_sh);
   const int D = p.D;
   const int Skv = p.Skv;
 
@@ -150,7 +161,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   const int kv_lo = p.window > 0 ? max(0, q0_abs - p.window + 1) : 0;
   const int kv_hi = p.causal ? min(Skv, ql_abs + 1) : Skv;
   const int t_begin = kv_lo / BN;
-  const int t_end = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN : t_begin;
+  const int nt = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN - t_begin : 0;
 
   const int qw0 = q0 + wave * 32;
   const int qrow = qw0 + l32;
@@ -159,14 +170,78 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   const int qwl_abs = p.q_offset + min(qw0 + 31, p.Sq - 1);
   const int qa = p.q_offset + qrow;
 
-  // Q^T as the B operand: lane holds row qrow, dims 16*ks + 8g .. +7.
+  // Scores stay in raw (q.k) units until the exponent: p = exp2(s*c - m*c).
+  const float c = SOFTCAP ? 1.0f : p.score_mul;
+  const float thresh = SOFTCAP ? kRescaleThresh : kRescaleThresh / p.score_mul;
+
+  // ---- direct global -> LDS tile loads -------------------------------------------
+  // Load j of this thread fills chunk position P = (4j + wave) * 64 + lane of the tile
+  // (each wave instruction writes 1 KiB of LDS); row = P / CPR, and the global chunk
+  // fetched is (P % CPR) ^ swz(row), clamped below head_dim (padding dims multiply a
+  // zero Q dim or feed O dims that are never stored).
+  const int dchunks = D >> 3;
+  uint32_t k_off[S::LPT], v_off[S::LPT];
+#pragma unroll
+  for (int j = 0; j < S::LPT; ++j) {
+    const int pos = (4 * j + wave) * 64 + lane;
+    const int row = pos / S::CPR;
+    const int q = pos - row * S::CPR;
+    const int kc = min(q ^ kswz<DP>(row), dchunks - 1);
+    const int vc = min(q ^ vswz<DP>(row), dchunks - 1);
+    k_off[j] = static_cast<uint32_t>(row * p.k_ss * 2 + kc * 16);
+    v_off[j] = static_cast<uint32_t>(row * p.v_ss * 2 + vc * 16);
+  }
+  auto issue_tile = [&](const char* base, int64_t stride, const uint32_t (&off)[S::LPT],
+                        uint16_t* dst, int t) {
+    const int kt0 = t * BN;
+    const char* tb = base + static_cast<int64_t>(kt0) * stride * 2;
+    if (kt0 + BN <= Skv) {
+#pragma unroll
+      for (int j = 0; j < S::LPT; ++j) {
+        load_lds16(tb + off[j], dst + (4 * j + wave) * 512);
+      }
+    } else {
+      // last tile: rows past Skv re-read row Skv-1 (their scores are masked to -inf)
+#pragma unroll
+      for (int j = 0; j < S::LPT; ++j) {
+        const int row = ((4 * j + wave) * 64 + lane) / S::CPR;
+        const int over = max(0, kt0 + row - (Skv - 1));
+        const int64_t back = static_cast<int64_t>(over) * stride * 2;
+        load_lds16(tb + off[j] - back, dst + (4 * j + wave) * 512);
+      }
+    }
+  };
+
+  // ---- per-lane LDS operand addresses (element offsets inside one tile buffer) ----
+  // K operand of k-step ks for 32-key block nb: row 32nb + l32, chunk 2ks + g.
+  int k_rd[S::KS];
+#pragma unroll
+  for (int ks = 0; ks < S::KS; ++ks) {
+    const int row = l32;
+    k_rd[ks] = row * DP + (((2 * ks + g) ^ kswz<DP>(row)) << 3);
+  }
+  // V^T operand of dim block db: this lane supplies row (key) rowoff of a 4-key group
+  // and dims colw .. colw+3 of the block (ds_read_b64_tr_b16 law: lanes 4k..4k+3 of a
+  // 16-lane group supply row k, lane i receives dim i of rows 0..3).
+  const int rowoff = 4 * g + ((lane & 15) >> 2);
+  const int colw = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int v_rd[S::DB];
+#pragma unroll
+  for (int db = 0; db < S::DB; ++db) {
+    const int cg = 4 * db + (colw >> 3);
+    v_rd[db] = rowoff * DP + ((cg ^ vswz<DP>(rowoff)) << 3) + (colw & 7);
+  }
+
+  // Q^T as the B operand: lane holds row qrow (clamped: rows past Sq are never
+  // stored), dims 16*ks + 8g .. +7.
   u32x4 qreg[S::KS];
   {
-    const bool rv = qrow < p.Sq;
-    const uint16_t* qr = qbase + static_cast<int64_t>(qrow) * p.q_ss;
+    const uint16_t* qr = qbase + static_cast<int64_t>(min(qrow, p.Sq - 1)) * p.q_ss;
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
-      qreg[ks] = rv ? load_row8(qr, 16 * ks + 8 * g, D, vec) : u32x4{0u, 0u, 0u, 0u};
+      const int d0 = min(16 * ks + 8 * g, D - 8);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + d0);
+      qreg[ks] = (16 * ks + 8 * g < D) ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
 
@@ -179,115 +254,59 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   float m_run = kNegInf;
   float l_run = 0.0f;
 
-  u32x4 kst[S::KPT];
-  u32x4 vst[S::VPT][4];
-
-  auto gload = [&](int t) {
-    const int kt0 = t * BN;
-#pragma unroll
-    for (int i = 0; i < S::KPT; ++i) {
-      const int idx = tid + i * kThreads;
-      if (idx < S::KCHUNKS) {
-        const int row = idx / (DP / 8);
-        const int c8 = idx - row * (DP / 8);
-        const int key = kt0 + row;
-        kst[i] = key < Skv ? load_row8(kbase + static_cast<int64_t>(key) * p.k_ss, c8 * 8, D, vec)
-                           : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < S::VPT; ++i) {
-      const int idx = tid + i * kThreads;
-      if (idx < S::VITEMS) {
-        const int kq = idx / (DP / 8);
-        const int c8 = idx - kq * (DP / 8);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = kt0 + 4 * kq + r;
-          vst[i][r] = key < Skv
-                          ? load_row8(vbase + static_cast<int64_t>(key) * p.v_ss, c8 * 8, D, vec)
-                          : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-    }
-  };
-
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < S::KPT; ++i) {
-      const int idx = tid + i * kThreads;
-      if (idx < S::KCHUNKS) {
-        const int row = idx / (DP / 8);
-        const int c8 = idx - row * (DP / 8);
-        *reinterpret_cast<u32x4*>(&k_lds[buf][row * S::KSTR + c8 * 8]) = kst[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < S::VPT; ++i) {
-      const int idx = tid + i * kThreads;
-      if (idx < S::VITEMS) {
-        const int kq = idx / (DP / 8);
-        const int c8 = idx - kq * (DP / 8);
-        u32x4 out[4];
-        quad_interleave(vst[i][0], vst[i][1], vst[i][2], vst[i][3], out);
-        u32x4* dst = reinterpret_cast<u32x4*>(&v_lds[buf][kq * S::VSTR + c8 * 32]);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) dst[w] = out[w];
-      }
-    }
-  };
-
-  auto compute = [&](int buf, int t) {
-    const int kt0 = t * BN;
-    if (!wave_live) return;
-    if (p.causal && kt0 > qwl_abs) return;
-    if (p.window > 0 && kt0 + BN - 1 < qw0_abs - p.window + 1) return;
-    const bool need_mask = (kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
-                           (p.window > 0 && kt0 < qwl_abs - p.window + 1);
-
-    f32x16 sacc[S::NB];
+  auto qk = [&](const uint16_t* kl, f32x16 (&sacc)[S::NB]) {
 #pragma unroll
     for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[nb][r] = 0.0f;
     }
-    const uint16_t* kl = &k_lds[buf][0];
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
 #pragma unroll
       for (int nb = 0; nb < S::NB; ++nb) {
-        const u32x4 a =
-            *reinterpret_cast<const u32x4*>(kl + (32 * nb + l32) * S::KSTR + 16 * ks + 8 * g);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(kl + k_rd[ks] + nb * 32 * DP);
         sacc[nb] = E::mfma32(a, qreg[ks], sacc[nb]);
       }
     }
+  };
 
+  // Online softmax of tile t (scores in sacc) then O^T += V^T P^T from V tile vl.
+  auto softmax_pv = [&](f32x16 (&sacc)[S::NB], int t, const uint16_t* vl) {
+    const int kt0 = t * BN;
+    if constexpr (SOFTCAP) {
+#pragma unroll
+      for (int nb = 0; nb < S::NB; ++nb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sacc[nb][r] = p.cap_mul * tanh_approx(sacc[nb][r] * p.score_mul);
+        }
+      }
+    }
+    const bool need_mask = (kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
+                           (p.window > 0 && kt0 < qwl_abs - p.window + 1);
+    if (need_mask) {
+#pragma unroll
+      for (int nb = 0; nb < S::NB; ++nb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kt0 + 32 * nb + 8 * (r >> 2) + 4 * g + (r & 3);
+          const bool ok = key < Skv && (!p.causal || key <= qa) &&
+                          (p.window <= 0 || key >= qa - p.window + 1);
+          sacc[nb][r] = ok ? sacc[nb][r] : kNegInf;
+        }
+      }
+    }
     float mt = kNegInf;
 #pragma unroll
     for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = sacc[nb][r];
-        if constexpr (SOFTCAP) {
-          x = p.cap_mul * tanh_approx(x * p.score_mul);
-        } else {
-          x = x * p.score_mul;
-        }
-        if (need_mask) {
-          const int key = kt0 + 32 * nb + 8 * (r >> 2) + 4 * g + (r & 3);
-          const bool ok = key < Skv && (!p.causal || key <= qa) &&
-                          (p.window <= 0 || key >= qa - p.window + 1);
-          x = ok ? x : kNegInf;
-        }
-        sacc[nb][r] = x;
-        mt = fmaxf(mt, x);
-      }
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[nb][r]);
     }
     mt = fmaxf(mt, wave_xor32(mt));
     const float m_new = fmaxf(m_run, mt);
-    const bool need = m_new > m_run + kRescaleThresh;
+    const bool need = m_new > m_run + thresh;
     if (__any(need)) {
-      const float alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
+      const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
       m_run = need ? m_new : m_run;
       l_run *= alpha;
 #pragma unroll
@@ -296,50 +315,58 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
         for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
       }
     }
-    const float mu = (m_run == kNegInf) ? 0.0f : m_run;
-
-    u32x4 pk[S::NC];
+    const float mc = (m_run == kNegInf) ? 0.0f : m_run * c;
 #pragma unroll
-    for (int c = 0; c < S::NC; ++c) {
-      const int nb = c >> 1;
-      const int base = (c & 1) * 8;
+    for (int cc = 0; cc < S::NC; ++cc) {
+      const int nb = cc >> 1;
+      const int base = (cc & 1) * 8;
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        pv[e] = fast_exp2(sacc[nb][base + e] - mu);
+        pv[e] = fast_exp2(fmaf(sacc[nb][base + e], c, -mc));
         l_run += pv[e];
       }
-      pk[c] = u32x4{E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
-                    E::pack2(pv[6], pv[7])};
-    }
-
-    const uint16_t* vl = &v_lds[buf][0];
-#pragma unroll
-    for (int c = 0; c < S::NC; ++c) {
-      const int kq0 = 4 * c + g;
-      const int kq1 = 4 * c + 2 + g;
+      const u32x4 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]),
+                        E::pack2(pv[4], pv[5]), E::pack2(pv[6], pv[7])};
 #pragma unroll
       for (int db = 0; db < S::DB; ++db) {
-        const int d = 32 * db + l32;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vl + kq0 * S::VSTR + d * 4);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vl + kq1 * S::VSTR + d * 4);
-        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-        oacc[db] = E::mfma32(a, pk[c], oacc[db]);
+        const uint16_t* r0 = vl + v_rd[db] + 16 * cc * DP;
+        const u32x2 lo2 = lds_read_tr16(r0);             // keys 16cc + 4g + 0..3
+        const u32x2 hi2 = lds_read_tr16(r0 + 8 * DP);    // keys 16cc + 8 + 4g + 0..3
+        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
+        oacc[db] = E::mfma32(a, pk, oacc[db]);
       }
     }
   };
 
-  if (t_begin < t_end) {
-    gload(t_begin);
-    lstore(0);
-  }
-  if (t_begin + 1 < t_end) gload(t_begin + 1);
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
+  f32x16 s_cur[S::NB];
+  f32x16 s_nxt[S::NB];
+  if (nt > 0) {
+    issue_tile(kbytes, p.k_ss, k_off, k_lds[0], t_begin);
+    issue_tile(vbytes, p.v_ss, v_off, v_lds[0], t_begin);
+    if (nt > 1) issue_tile(kbytes, p.k_ss, k_off, k_lds[1], t_begin + 1);
+    wait_vmcnt0();
     __syncthreads();
-    if (t + 1 < t_end) lstore(buf ^ 1);
-    if (t + 2 < t_end) gload(t + 2);
-    compute(buf, t);
+    if (wave_live) qk(k_lds[0], s_cur);
+  }
+  // Iteration i computes tile t = t_begin + i. Entering it, K(t+1) and V(t) are in
+  // LDS; it issues K(t+2) and V(t+1) into the buffers iteration i-1 finished reading,
+  // computes S^T(t+1) (MFMA) ahead of softmax(t) (VALU), then P V(t). The loop body is
+  // written twice so the two score buffers swap roles without copies.
+  auto step = [&](int i, f32x16 (&cur)[S::NB], f32x16 (&nxt)[S::NB]) {
+    const int t = t_begin + i;
+    wait_vmcnt0();
+    __syncthreads();
+    if (i + 2 < nt) issue_tile(kbytes, p.k_ss, k_off, k_lds[i & 1], t + 2);
+    if (i + 1 < nt) issue_tile(vbytes, p.v_ss, v_off, v_lds[(i + 1) & 1], t + 1);
+    if (!wave_live) return;
+    if (p.causal && t * BN > qwl_abs) return;  // past this wave's causal band
+    if (i + 1 < nt) qk(k_lds[(i + 1) & 1], nxt);
+    softmax_pv(cur, t, v_lds[i & 1]);
+  };
+  for (int i = 0; i < nt; i += 2) {
+    step(i, s_cur, s_nxt);
+    if (i + 1 < nt) step(i + 1, s_nxt, s_cur);
   }
 
   const float l_tot = l_run + wave_xor32(l_run);
@@ -353,22 +380,12 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
         const int d0 = 32 * db + 8 * i + 4 * g;
         const uint32_t w0 = E::pack2(oacc[db][4 * i + 0] * inv, oacc[db][4 * i + 1] * inv);
         const uint32_t w1 = E::pack2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
-        if (vec && d0 + 4 <= D) {
-          *reinterpret_cast<u32x2*>(orow + d0) = u32x2{w0, w1};
-        } else {
-          const uint16_t hv[4] = {static_cast<uint16_t>(w0 & 0xffffu),
-                                  static_cast<uint16_t>(w0 >> 16),
-                                  static_cast<uint16_t>(w1 & 0xffffu),
-                                  static_cast<uint16_t>(w1 >> 16)};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            if (d0 + j < D) orow[d0 + j] = hv[j];
-          }
-        }
+        if (d0 < D) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{w0, w1};
       }
     }
     if (p.lse != nullptr && g == 0) {
-      const float lse = l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : masked_row_lse(p, qrow);
+      const float lse = l_tot > 0.0f ? (m_run * c + fast_log2(l_tot)) * kLn2
+                                     : masked_row_lse(p, qrow);
       p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(qrow) * p.l_ss] = lse;
     }
   }
@@ -447,16 +464,9 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   p.ref_bkv = a.ref_block_kv > 0 ? a.ref_block_kv : 64;
   p.masked_lse_mode = a.masked_lse_mode;
 
-  bool vec = (a.head_dim % 8) == 0 && aligned16(a.q) && aligned16(a.k) && aligned16(a.v) &&
-             aligned16(a.o);
-  const int64_t* strides[4] = {a.q_stride, a.k_stride, a.v_stride, a.o_stride};
-  for (int t = 0; t < 4 && vec; ++t) {
-    for (int i = 0; i < 3; ++i) {
-      if (strides[t][i] % 8 != 0) vec = false;
-    }
-  }
-  p.vec = vec ? 1 : 0;
-
+  // The kernels move 16-byte chunks: callers guarantee 16-byte aligned bases, strides
+  // that are multiples of 8 elements and head_dim % 8 == 0 (checked by ffa_prefill_fwd),
+  // and per-tile byte offsets that fit 32 bits.
   const int64_t grid64 = static_cast<int64_t>(p.n_qt) * a.batch * a.heads_q;
   if (grid64 <= 0) return FFA_OK;
   if (grid64 > 0x7fffffff) return FFA_ERR_TOO_LARGE;

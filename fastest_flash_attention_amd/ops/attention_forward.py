@@ -66,10 +66,22 @@ class PrefillCall:
     out: torch.Tensor
     lse: Optional[torch.Tensor]
     squeezed: bool
+    d_user: int = 0
 
 
-def _unit_last(t: torch.Tensor) -> torch.Tensor:
-    return t if t.stride(-1) == 1 or t.size(-1) == 1 else t.contiguous()
+def _conform(t: torch.Tensor, d_pad: int) -> torch.Tensor:
+    """Return ``t`` (or a copy) in the form the kernels load in 16-byte chunks: unit
+    dim stride, 16-byte aligned base, batch/head/seq strides multiple of 8 elements,
+    dim zero-padded to ``d_pad`` (zeros leave q.k and the stored O dims unchanged)."""
+    if t.size(-1) != d_pad:
+        return torch.nn.functional.pad(t, (0, d_pad - t.size(-1))).contiguous()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all(st % 8 == 0 for st, n in zip(t.stride()[:3], t.shape[:3]) if n > 1))
+    if ok:
+        return t
+    out = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    out.copy_(t)
+    return out
 
 
 def _batch_strides(t: torch.Tensor, B: int, name: str) -> list[int]:
@@ -223,17 +235,23 @@ def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> Pref
     code = _lib.dtype_code(r.q.dtype)
     if r.D > 256:
         raise ValueError(f"head_dim {r.D} > 256 is not supported")
-    r.q = _unit_last(r.q)
-    r.k = _unit_last(r.k)
-    r.v = _unit_last(r.v)
-    if out is None:
-        out = torch.empty((r.B, r.H_q, r.S_q, r.D), dtype=r.q.dtype, device=r.q.device)
+    d_pad = (r.D + 7) // 8 * 8
+    r.q = _conform(r.q, d_pad)
+    r.k = _conform(r.k, d_pad)
+    r.v = _conform(r.v, d_pad)
+    d_user = r.D
+    r.D = d_pad
+    if out is None or d_pad != d_user:
+        out = torch.empty((r.B, r.H_q, r.S_q, d_pad), dtype=r.q.dtype, device=r.q.device)
     lse = (
         torch.empty((r.B, r.H_q, r.S_q, 1), dtype=torch.float32, device=r.q.device)
         if r.return_lse
         else None
     )
-    return PrefillCall(build_prefill_args(r, out, lse, code), r.q, r.k, r.v, out, lse, r.squeezed)
+    call = PrefillCall(build_prefill_args(r, out, lse, code), r.q, r.k, r.v, out, lse,
+                       r.squeezed)
+    call.d_user = d_user
+    return call
 
 
 def launch_prefill(call: PrefillCall) -> None:
@@ -277,6 +295,8 @@ def fastest_flash_attn_forward(
     )
     launch_prefill(call)
     output, lse = call.out, call.lse
+    if output.size(-1) != call.d_user:
+        output = output[..., : call.d_user].contiguous()
     if call.squeezed:
         output = output.squeeze(1)
         if lse is not None:

@@ -42,7 +42,8 @@ typedef enum ffa_status {
   FFA_ERR_INVALID_ARG = -1,      /* null pointer, non-positive size, bad stride, ... */
   FFA_ERR_UNSUPPORTED_DTYPE = -2,
   FFA_ERR_UNSUPPORTED_HEAD_DIM = -3,
-  FFA_ERR_MISALIGNED = -4,       /* reserved: misaligned operands take a scalar path */
+  FFA_ERR_MISALIGNED = -4,       /* base not 16-byte aligned, or head_dim / a stride not a
+                                    multiple of 8 elements (prefill) */
   FFA_ERR_GQA_RATIO = -5,        /* heads_q not a multiple of heads_kv */
   FFA_ERR_WORKSPACE = -6,        /* decode workspace missing or too small */
   FFA_ERR_LAUNCH = -7,           /* hipGetLastError() reported a launch failure */
@@ -73,7 +74,9 @@ typedef enum ffa_dtype {
  * GQA: q head h reads kv head h / (heads_q / heads_kv)  (utils.py:111-130).
  * Layout: element strides per tensor in order [batch, head, seq, dim]; the dim
  * stride must be 1. A batch or head stride may be 0 (broadcast). lse strides are
- * [batch, head, seq]. q/k/v/o share the dtype.
+ * [batch, head, seq]. q/k/v/o share the dtype. q/k/v/o are 16-byte aligned, head_dim
+ * and the batch/head/seq strides are multiples of 8 elements (FFA_ERR_MISALIGNED
+ * otherwise), and k/v seq strides are below 2^24 elements.
  */
 typedef struct ffa_prefill_args {
   const void* q;

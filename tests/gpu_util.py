@@ -75,4 +75,8 @@ def probe_lib():
     for name in ("ffa_probe_mfma32", "ffa_probe_mfma16"):
         getattr(lib, name).restype = ctypes.c_int
         getattr(lib, name).argtypes = [ctypes.c_void_p] * 3
+    lib.ffa_probe_tr16.restype = ctypes.c_int
+    lib.ffa_probe_tr16.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    lib.ffa_probe_load_lds.restype = ctypes.c_int
+    lib.ffa_probe_load_lds.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     return lib

@@ -51,3 +51,46 @@ extern "C" int ffa_probe_mfma16(const void* A, const void* B, void* out) {
                      static_cast<const uint16_t*>(B), static_cast<float*>(out));
   return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }
+
+// ds_read_b64_tr_b16: LDS holds elements 0..1023 (value = index). Lane l reads
+// 64 bits at element address addr(l); out[l][0..3] are the element indices returned.
+//   mode 0: addr(l) = 4 l                      (64 rows x 4 elements, row-major)
+//   mode 1: addr(l) = 64 (l % 16) + 4 (l / 16) (16 rows of 64 elements per group)
+// Every address stays inside the 1024-element LDS array.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__global__ void probe_tr16(int mode, short* out) {
+  __shared__ __attribute__((aligned(16))) short lds[1024];
+  const int l = threadIdx.x;
+  for (int i = l; i < 1024; i += 64) lds[i] = static_cast<short>(i);
+  __syncthreads();
+  const int addr = mode == 0 ? 4 * l : 64 * (l % 16) + 4 * (l / 16);
+  typedef __attribute__((address_space(3))) short lds_short;
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((lds_short*)lds + addr));
+  for (int e = 0; e < 4; ++e) out[l * 4 + e] = v[e];
+}
+
+// global_load_lds_dwordx4: lane l loads the 16-byte chunk (63 - l) of a 1 KiB global
+// buffer; the LDS image (1 KiB) is copied out.
+__global__ void probe_load_lds(const unsigned* g, unsigned* out) {
+  __shared__ __attribute__((aligned(16))) unsigned lds[256];
+  const int l = threadIdx.x;
+  for (int i = l; i < 256; i += 64) lds[i] = 0xdeadbeefu;
+  __syncthreads();
+  __builtin_amdgcn_global_load_lds(g + (63 - l) * 4,
+                                   (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int i = l; i < 256; i += 64) out[i] = lds[i];
+}
+
+extern "C" int ffa_probe_tr16(int mode, void* out) {
+  hipLaunchKernelGGL(probe_tr16, dim3(1), dim3(64), 0, 0, mode, static_cast<short*>(out));
+  return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int ffa_probe_load_lds(const void* g, void* out) {
+  hipLaunchKernelGGL(probe_load_lds, dim3(1), dim3(64), 0, 0, static_cast<const unsigned*>(g),
+                     static_cast<unsigned*>(out));
+  return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}

@@ -46,3 +46,36 @@ def test_mfma_16x16x32_layout():
     for lane in range(64):
         for j in range(4):
             assert got[lane, j] == C[4 * (lane // 16) + j, lane % 16], (lane, j)
+
+
+def test_global_load_lds_lane_placement():
+    """global_load_lds_dwordx4: lane l's 16 bytes land at LDS base + 16 l."""
+    require_gpu()
+    lib = probe_lib()
+    g = torch.arange(256, dtype=torch.int32, device="cuda")
+    out = torch.zeros(256, dtype=torch.int32, device="cuda")
+    say("global_load_lds probe")
+    assert lib.ffa_probe_load_lds(g.data_ptr(), out.data_ptr()) == 0
+    got = out.cpu().numpy().reshape(64, 4)
+    want = np.arange(256).reshape(64, 4)[::-1]
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_ds_read_tr16_b64_layout(mode):
+    """Records the element each lane receives from ds_read_b64_tr_b16 (printed) and
+    checks the transpose law the V operand loader relies on: within each group of 16
+    lanes, lane i receives element (i % 4) ... see the kernel comment."""
+    require_gpu()
+    lib = probe_lib()
+    out = torch.zeros(256, dtype=torch.int16, device="cuda")
+    say(f"ds_read_tr16 probe mode {mode}")
+    assert lib.ffa_probe_tr16(mode, out.data_ptr()) == 0
+    got = out.cpu().numpy().reshape(64, 4)
+    print(f"tr16 mode {mode}:")
+    for l in range(64):
+        print(l, got[l].tolist())
+    # every element read must come from one of the 64 lanes' own 4-element windows
+    addrs = [4 * l if mode == 0 else 64 * (l % 16) + 4 * (l // 16) for l in range(64)]
+    window = {a + e for a in addrs for e in range(4)}
+    assert set(got.flatten().tolist()) <= window
