@@ -143,6 +143,14 @@ int ffa_paged_decode_fwd(const ffa_paged_decode_args* a, void* stream) {
     }
   }
   if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  if (a->max_context_len > 0 && a->num_pages < 1) return FFA_ERR_INVALID_ARG;
+  // 16-byte loads of q rows, K rows (to registers) and V rows (to LDS)
+  if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
+  const void* ptrs[3] = {a->q, a->k_pages, a->v_pages};
+  for (const void* ptr : ptrs) {
+    if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) return FFA_ERR_MISALIGNED;
+  }
+  if (a->q_stride[0] % 8 != 0 || a->q_stride[1] % 8 != 0) return FFA_ERR_MISALIGNED;
   const size_t need = ffa::decode_workspace_bytes(a->batch, a->heads_q, a->head_dim,
                                                   a->max_context_len, a->tokens_per_split);
   if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need)) return FFA_ERR_WORKSPACE;

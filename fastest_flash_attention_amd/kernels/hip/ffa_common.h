@@ -142,4 +142,12 @@ __device__ inline u32x2 lds_read_tr16(const uint16_t* lds_ptr) {
 
 __device__ inline void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding: N[3:0] in bits 3:0, N[5:4] in bits 15:14).
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+__device__ inline void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 }  // namespace ffa

@@ -9,24 +9,23 @@
 //   split kernel  grid (splits, Hkv * column_groups, batch), 4 waves per workgroup.
 //                 A workgroup streams tokens_per_split tokens of one (sequence, KV head)
 //                 straight from the pages; every K/V byte is read once and serves all
-//                 G query heads of the group (no repeat_kv).
-//                 Per 32-token tile, wave-level:
-//                   S^T[key, head] = K Q^T    v_mfma_f32_16x16x32: K (A operand) is
-//                                  loaded from HBM directly in operand layout: a lane
-//                                  reads 16 B of one token row, 16 lanes cover 16 rows x
-//                                  64 B, so every 128-bit load is fully used;
-//                   softmax        fp32, exp2, max/sum via lane swaps (xor 16, 32),
-//                                  rescale deferred until the max grows by 2^8;
-//                   O^T += V^T P^T V staged through a per-wave LDS region in key-quad
-//                                  order ([key/4][dim][4 keys]) so its A operand is two
-//                                  8-byte LDS reads; P comes straight from the S^T
-//                                  accumulators.
-//                 The next tile's K/V loads are issued before the current tile is
-//                 computed. The 4 waves' partials are merged through LDS and one
+//                 G query heads of the group (no repeat_kv). The block-table entries of
+//                 the split are staged in LDS first, so no tile waits on a dependent
+//                 block-table load. Each wave owns every 4th 32-token tile and keeps two
+//                 tiles in flight:
+//                   K  HBM -> registers in MFMA A-operand layout (a lane reads 16 B of
+//                      one token row, 16 lanes cover 16 rows x 64 B);
+//                   V  HBM -> LDS by global_load_lds_dwordx4 (no VGPR staging), rows
+//                      XOR-swizzled, read back transposed by ds_read_b64_tr_b16.
+//                 Per tile: S^T[key, head] = K Q^T (v_mfma_f32_16x16x32), fp32 softmax
+//                 with exp2 and lane swaps (xor 16, 32), rescale deferred until the max
+//                 grows by 2^8, O^T += V^T P^T with P taken straight from the S^T
+//                 accumulators. The 4 waves' partials are merged through LDS and one
 //                 normalised (O, lse) partial per query head goes to the workspace.
 //   combine kernel one wave per (sequence, query head): O = sum_s exp(lse_s - lse) O_s,
 //                 lse = logsumexp_s lse_s.
-// Page ids outside [0, num_pages) read as zeros instead of faulting.
+// Page ids outside [0, num_pages) read page 0 of the pool's first head instead of
+// faulting (their keys still count); block tables are the caller's contract.
 
 #include "ffa_common.h"
 #include "ffa_internal.h"
@@ -38,7 +37,8 @@ constexpr int kDecThreads = 256;
 constexpr int kDecWaves = 4;
 constexpr int kTile = 32;            // tokens per wave tile
 constexpr int kCols = 16;            // query heads per workgroup (MFMA N)
-constexpr int kDefaultSplit = 512;   // tokens per split
+constexpr int kDefaultSplit = 1024;  // tokens per split
+constexpr int kMaxSplit = 2048;      // bounds the LDS block-table stage
 constexpr int kMinSplit = 32;
 constexpr float kRescaleThresh = 8.0f;
 
@@ -62,7 +62,6 @@ struct DecodeParams {
   int n_cg;
   int dp;
   float score_mul, cap_mul;
-  int vec;
 };
 
 template <int DP>
@@ -85,32 +84,33 @@ __device__ inline int page_of(const DecodeParams& p, int tok, int& slot) {
   return pi;
 }
 
-// Row pointer of token `tok` (must be < context length) in `pool`, or nullptr when
-// the block table names a page outside the pool.
-__device__ inline const uint16_t* token_row(const DecodeParams& p, const uint16_t* pool,
-                                            const int32_t* btrow, int hk, int tok) {
-  int slot;
-  const int pi = page_of(p, tok, slot);
-  const int phys = btrow[pi];
-  if (phys < 0 || phys >= p.num_pages) return nullptr;
-  return pool + static_cast<int64_t>(phys) * p.page_stride + hk * p.head_stride +
-         static_cast<int64_t>(slot) * p.D;
-}
-
-// head_dim <= 128: two workgroups per CU; wider heads keep twice the K/V tile in
-// registers and run one wave per SIMD.
 template <int DP>
 constexpr int kDecMinBlocks = DP <= 128 ? 2 : 1;
+
+// XOR swizzle (16-byte chunk index) of the V rows in LDS: the 8 rows x 32 bytes a
+// transposed read fetches per half-wave land in distinct bank groups.
+template <int DP>
+__device__ inline int dec_vswz(int r) {
+  if constexpr (DP == 32) return 2 * ((r >> 2) & 1);
+  if constexpr (DP == 64 || DP == 192) return 2 * ((r >> 1) & 3);
+  return 2 * (r & 7);
+}
 
 template <typename Tag, int DP, bool SOFTCAP>
 __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_kernel(
     const DecodeParams p) {
   using S = DShape<DP>;
   using E = Elem<Tag>;
-  // V staging during the sweep; reused for the wave merge afterwards.
-  constexpr int kVBytes = kDecWaves * S::V_ELEMS * 2;
+  constexpr int CPR = DP / 8;                    // 16-byte chunks per row
+  constexpr int VTILE = kTile * DP;              // elements of one V tile
+  constexpr int VLOADS = kTile * CPR / 64;       // V direct loads per lane per tile
+  constexpr int KLOADS = 2 * S::KS;              // K register loads per lane per tile
+  constexpr int NL = VLOADS + KLOADS;            // vector memory ops per lane per tile
+  // V stages (2 per wave) during the sweep; reused for the wave merge afterwards.
+  constexpr int kVBytes = kDecWaves * 2 * VTILE * 2;
   constexpr int kRedBytes = kDecWaves * kCols * (DP + 1) * 4;
-  __shared__ __attribute__((aligned(16))) char smem[kVBytes > kRedBytes ? kVBytes : kRedBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kVBytes > kRedBytes ? kVBytes : kRedBytes];
+  __shared__ int bt_lds[kMaxSplit + 2];
   __shared__ float red_m[kDecWaves][kCols];
   __shared__ float red_l[kDecWaves][kCols];
   auto red_o = reinterpret_cast<float(*)[kCols][DP + 1]>(smem);
@@ -132,20 +132,46 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   const int g4 = lane >> 4;   // 0..3
   const int gcols = min(kCols, p.G - cg * kCols);
   const int head0 = hk * p.G + cg * kCols;
-  const bool col_live = c16 < gcols;
-  const bool vec = p.vec != 0;
   const int D = p.D;
-  const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+  const int dchunks = D >> 3;
+
+  // Stage the split's physical page ids (entries [pg0, pg1]) in LDS.
+  int slot0;
+  const int pg0 = page_of(p, s_begin, slot0);
+  int slot1;
+  const int pg1 = page_of(p, s_end - 1, slot1);
+  {
+    const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+    for (int i = tid; i <= pg1 - pg0; i += kDecThreads) {
+      const int phys = btrow[pg0 + i];
+      bt_lds[i] = (phys >= 0 && phys < p.num_pages) ? phys : 0;
+    }
+  }
+  const char* kpool = reinterpret_cast<const char*>(p.kp);
+  const char* vpool = reinterpret_cast<const char*>(p.vp);
+  // byte offset of token `tok` (clamped into the split) of this KV head in a pool
+  auto row_off = [&](int tok) -> int64_t {
+    tok = min(tok, s_end - 1);
+    int slot;
+    const int pg = page_of(p, tok, slot);
+    const int phys = bt_lds[pg - pg0];
+    return (static_cast<int64_t>(phys) * p.page_stride + hk * p.head_stride +
+            static_cast<int64_t>(slot) * D) * 2;
+  };
 
   // Q^T as the B operand: lane holds head (head0 + c16), dims 32*ks + 8*g4 .. +7.
   u32x4 qreg[S::KS];
   {
-    const uint16_t* qr = p.q + b * p.q_sb + (head0 + c16) * p.q_sh;
+    const bool col_live = c16 < gcols;
+    const uint16_t* qr = p.q + b * p.q_sb + (col_live ? head0 + c16 : head0) * p.q_sh;
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
-      qreg[ks] = col_live ? load_row8(qr, 32 * ks + 8 * g4, D, vec) : u32x4{0u, 0u, 0u, 0u};
+      const int d0 = min(32 * ks + 8 * g4, D - 8);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + d0);
+      qreg[ks] = (col_live && 32 * ks + 8 * g4 < D) ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
+  __syncthreads();  // bt_lds ready
 
   f32x4 oacc[S::DB];
 #pragma unroll
@@ -154,71 +180,60 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   float l_run = 0.0f;
 
   const int n_tiles = (s_end - s_begin + kTile - 1) / kTile;
-  uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + wave * S::V_ELEMS;
+  uint16_t* vstage = reinterpret_cast<uint16_t*>(smem) + wave * 2 * VTILE;
+  u32x4 kreg0[2][S::KS];  // K of the stage-0 tile (registers), stage 1 below
+  u32x4 kreg1[2][S::KS];
 
-  u32x4 kreg[2][S::KS];
-  u32x4 vreg[S::VPL][4];
+  // Per-lane constants of the V direct loads: load j fills chunk position
+  // j * 64 + lane of the tile -> row, swizzled source chunk.
+  int vrow[VLOADS];
+  int vchk[VLOADS];
+#pragma unroll
+  for (int j = 0; j < VLOADS; ++j) {
+    const int pos = j * 64 + lane;
+    vrow[j] = pos / CPR;
+    vchk[j] = min((pos - vrow[j] * CPR) ^ dec_vswz<DP>(vrow[j]), dchunks - 1);
+  }
+  // Per-lane V^T operand addresses (elements) of dim block db inside a V tile: this
+  // lane supplies row 4*g4 + (c16 >> 2) of a 4-key group and dims 4*(c16 & 3) .. +3
+  // of the 16-dim block (ds_read_b64_tr_b16 law).
+  const int vr = 4 * g4 + (c16 >> 2);
+  int vrd[S::DB];
+#pragma unroll
+  for (int db = 0; db < S::DB; ++db) {
+    const int col = 16 * db + 4 * (c16 & 3);
+    vrd[db] = vr * DP + (((col >> 3) ^ dec_vswz<DP>(vr)) << 3) + (col & 7);
+  }
 
-  auto gload = [&](int it) {
+  auto issue = [&](int it, int st, u32x4 (&kreg)[2][S::KS]) {
     const int t0 = s_begin + it * kTile;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      const int tok = t0 + 16 * sub + c16;
-      const uint16_t* row = tok < s_end ? token_row(p, p.kp, btrow, hk, tok) : nullptr;
+      const char* row = kpool + row_off(t0 + 16 * sub + c16);
 #pragma unroll
       for (int ks = 0; ks < S::KS; ++ks) {
-        kreg[sub][ks] =
-            row != nullptr ? load_row8(row, 32 * ks + 8 * g4, D, vec) : u32x4{0u, 0u, 0u, 0u};
+        const int d0 = min(32 * ks + 8 * g4, D - 8);
+        kreg[sub][ks] = *reinterpret_cast<const u32x4*>(row + d0 * 2);
       }
     }
+    uint16_t* dst = vstage + st * VTILE;
 #pragma unroll
-    for (int i = 0; i < S::VPL; ++i) {
-      const int item = lane + 64 * i;
-      if (item < S::VITEMS) {
-        const int kq = item / (DP / 8);
-        const int c8 = item - kq * (DP / 8);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tok = t0 + 4 * kq + r;
-          const uint16_t* row = tok < s_end ? token_row(p, p.vp, btrow, hk, tok) : nullptr;
-          vreg[i][r] = row != nullptr ? load_row8(row, c8 * 8, D, vec) : u32x4{0u, 0u, 0u, 0u};
-        }
-      }
+    for (int j = 0; j < VLOADS; ++j) {
+      load_lds16(vpool + row_off(t0 + vrow[j]) + vchk[j] * 16, dst + j * 512);
     }
   };
 
-  int it = wave;
-  if (it < n_tiles) gload(it);
-  for (; it < n_tiles; it += kDecWaves) {
-    // V of this tile -> LDS (key quads); K of this tile stays in registers.
-#pragma unroll
-    for (int i = 0; i < S::VPL; ++i) {
-      const int item = lane + 64 * i;
-      if (item < S::VITEMS) {
-        const int kq = item / (DP / 8);
-        const int c8 = item - kq * (DP / 8);
-        u32x4 out[4];
-        quad_interleave(vreg[i][0], vreg[i][1], vreg[i][2], vreg[i][3], out);
-        u32x4* dst = reinterpret_cast<u32x4*>(vl + kq * S::VSTR + c8 * 32);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) dst[w] = out[w];
-      }
-    }
-    u32x4 kc[2][S::KS];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-      for (int ks = 0; ks < S::KS; ++ks) kc[sub][ks] = kreg[sub][ks];
-    }
+  auto compute = [&](int it, int st, const u32x4 (&kreg)[2][S::KS]) {
     const int t0 = s_begin + it * kTile;
-    if (it + kDecWaves < n_tiles) gload(it + kDecWaves);
-
     f32x4 sacc[2];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       sacc[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < S::KS; ++ks) sacc[sub] = E::mfma16(kc[sub][ks], qreg[ks], sacc[sub]);
+      for (int ks = 0; ks < S::KS; ++ks) {
+        // dims >= head_dim of K were clamped re-reads: the zero Q dims cancel them
+        sacc[sub] = E::mfma16(kreg[sub][ks], qreg[ks], sacc[sub]);
+      }
     }
     float mt = kNegInf;
 #pragma unroll
@@ -263,20 +278,44 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
     }
     const u32x4 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
                       E::pack2(pv[6], pv[7])};
+    const uint16_t* vl = vstage + st * VTILE;
 #pragma unroll
     for (int db = 0; db < S::DB; ++db) {
-      const int d = 16 * db + c16;
-      const u32x2 a0 = *reinterpret_cast<const u32x2*>(vl + g4 * S::VSTR + d * 4);
-      const u32x2 a1 = *reinterpret_cast<const u32x2*>(vl + (4 + g4) * S::VSTR + d * 4);
+      const u32x2 a0 = lds_read_tr16(vl + vrd[db]);            // keys 4*g4 + 0..3
+      const u32x2 a1 = lds_read_tr16(vl + vrd[db] + 16 * DP);  // keys 16 + 4*g4 + 0..3
       const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
       oacc[db] = E::mfma16(a, pk, oacc[db]);
     }
+  };
+
+  // Wave w owns tiles w, w + 4, ...; its i-th tile uses stage i & 1 (the loop is
+  // written for both stages so register arrays are never indexed at run time).
+  // Entering the compute of tile i, tiles i and i+1 are in flight: waiting until at
+  // most one tile's NL memory ops remain leaves tile i complete (in-order counter).
+  const int my_tiles = n_tiles > wave ? (n_tiles - wave + kDecWaves - 1) / kDecWaves : 0;
+  if (my_tiles > 0) issue(wave, 0, kreg0);
+  if (my_tiles > 1) issue(wave + kDecWaves, 1, kreg1);
+  auto step = [&](int i, int st, u32x4 (&kreg)[2][S::KS]) {
+    if (i + 1 < my_tiles) {
+      wait_vmcnt<NL>();
+    } else {
+      wait_vmcnt0();
+    }
+    compute(wave + i * kDecWaves, st, kreg);
+    if (i + 2 < my_tiles) {
+      wait_lgkmcnt0();  // this stage's transposed reads are done before it is refilled
+      issue(wave + (i + 2) * kDecWaves, st, kreg);
+    }
+  };
+  for (int i = 0; i < my_tiles; i += 2) {
+    step(i, 0, kreg0);
+    if (i + 1 < my_tiles) step(i + 1, 1, kreg1);
   }
 
   // Per-wave totals, then merge the 4 waves through LDS.
   float l_w = l_run + __shfl_xor(l_run, 16);
   l_w += __shfl_xor(l_w, 32);
-  __syncthreads();  // every wave is done with its V staging region
+  __syncthreads();  // every wave is done with its V stages
   if (g4 == 0) {
     red_m[wave][c16] = m_run;
     red_l[wave][c16] = l_w;
@@ -424,7 +463,7 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 int32_t decode_tokens_per_split(int32_t tokens_per_split) {
   if (tokens_per_split <= 0) return kDefaultSplit;
   const int32_t t = ((tokens_per_split + kTile - 1) / kTile) * kTile;
-  return t < kMinSplit ? kMinSplit : t;
+  return t < kMinSplit ? kMinSplit : (t > kMaxSplit ? kMaxSplit : t);
 }
 
 int32_t decode_num_splits(int32_t max_context_len, int32_t tokens_per_split) {
@@ -479,9 +518,6 @@ int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream) {
     p.score_mul = a.scale * kLog2e;
     p.cap_mul = 0.0f;
   }
-  const bool vec = (a.head_dim % 8) == 0 && aligned16(a.q) && aligned16(a.k_pages) &&
-                   aligned16(a.v_pages) && (a.q_stride[0] % 8) == 0 && (a.q_stride[1] % 8) == 0;
-  p.vec = vec ? 1 : 0;
   const size_t rows = static_cast<size_t>(a.batch) * a.heads_q * p.n_splits;
   p.ws_o = static_cast<float*>(a.workspace);
   p.ws_lse = p.ws_o + rows * p.dp;

@@ -29,10 +29,11 @@ from ..kernels import _lib
 
 
 def _auto_tokens_per_split(batch: int, heads_kv: int, max_len: int) -> int:
-    """Largest split (<= 512 tokens, >= 64) that still yields >= 2048 workgroups, so
-    small batches keep all 256 CUs streaming."""
-    tps = 512
-    while tps > 64 and batch * heads_kv * max(1, math.ceil(max_len / tps)) < 2048:
+    """Largest split (<= 2048 tokens, >= 64) that still yields >= 1024 workgroups, so
+    small batches keep all 256 CUs streaming while long contexts amortise each
+    workgroup's pipeline fill."""
+    tps = 2048
+    while tps > 64 and batch * heads_kv * max(1, math.ceil(max_len / tps)) < 1024:
         tps //= 2
     return tps
 
@@ -96,14 +97,16 @@ def fastest_flash_paged_decode(
     if not (q3.dtype == k_pages.dtype == v_pages.dtype):
         raise TypeError("q and the page pools must share a dtype")
     code = _lib.dtype_code(q3.dtype)
+    if D % 8 != 0:
+        raise ValueError(f"paged decode needs head_dim % 8 == 0 (got {D})")
     if not (k_pages.is_contiguous() and v_pages.is_contiguous()):
         raise ValueError("page pools must be contiguous")
     if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
         raise TypeError("block_tables and context_lens must be int32")
     block_tables = block_tables.contiguous()
     context_lens = context_lens.contiguous()
-    if q3.stride(-1) != 1:
-        q3 = q3.contiguous()
+    if q3.stride(-1) != 1 or q3.data_ptr() % 16 or q3.stride(0) % 8 or q3.stride(1) % 8:
+        q3 = q3.contiguous() if not q3.is_contiguous() else q3.clone()
     if max_context_len is None:
         max_context_len = int(context_lens.max().item()) if B > 0 else 0
     if block_tables.size(1) * page_size < max_context_len:

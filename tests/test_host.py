@@ -178,7 +178,7 @@ def test_validation_errors_without_device(lib):
     assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -1  # null pointers
     d = _lib.PagedDecodeArgs()
     d.dtype, d.head_dim, d.batch, d.heads_q, d.heads_kv, d.page_size = 0, 128, 2, 8, 2, 16
-    d.max_context_len, d.block_table_stride = 64, 4
+    d.max_context_len, d.block_table_stride, d.num_pages = 64, 4, 8
     d.q = d.o = d.k_pages = d.v_pages = d.block_tables = d.context_lens = 16
     d.workspace, d.workspace_bytes = 16, 8
     assert lib.ffa_paged_decode_fwd(ctypes.byref(d), None) == -6
@@ -192,7 +192,8 @@ def test_validation_errors_without_device(lib):
 def test_workspace_sizing(lib):
     # [B][Hq][splits][Dpad] O partials + [B][Hq][splits] lse, fp32
     assert lib.ffa_paged_decode_num_splits(32768, 512) == 64
-    assert lib.ffa_paged_decode_num_splits(1000, 0) == 2  # default split 512
+    assert lib.ffa_paged_decode_num_splits(1000, 0) == 1  # default split 1024
+    assert lib.ffa_paged_decode_num_splits(5000, 4096) == 3  # split clamped to 2048
     assert lib.ffa_paged_decode_workspace_bytes(64, 32, 128, 32768, 512) == 64 * 32 * 64 * 129 * 4
     assert lib.ffa_paged_decode_workspace_bytes(2, 4, 100, 100, 64) == 2 * 4 * 2 * 129 * 4
 
