@@ -243,10 +243,12 @@ def main() -> int:
         return 1
     torch.cuda.set_device(0)
     if args.calibrate_copy_mib > 0:
-        src = torch.ones(args.calibrate_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        # one elementwise kernel reading and writing exactly N MiB (fp32 negate)
+        src = torch.ones((args.calibrate_copy_mib << 20) // 4, dtype=torch.float32,
+                         device="cuda")
         dst = torch.empty_like(src)
         torch.cuda.synchronize()
-        dst.copy_(src)
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
     pre = bench_prefill(args.workload, args.steps, args.warmup, args.cpu_seconds)

@@ -260,13 +260,25 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[nb][r] = 0.0f;
     }
+    // K operands one k-step ahead of the MFMAs that consume them
+    u32x4 a_cur[S::NB], a_nxt[S::NB];
+#pragma unroll
+    for (int nb = 0; nb < S::NB; ++nb) {
+      a_cur[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd[0] + nb * 32 * DP);
+    }
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
+      if (ks + 1 < S::KS) {
 #pragma unroll
-      for (int nb = 0; nb < S::NB; ++nb) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(kl + k_rd[ks] + nb * 32 * DP);
-        sacc[nb] = E::mfma32(a, qreg[ks], sacc[nb]);
+        for (int nb = 0; nb < S::NB; ++nb) {
+          a_nxt[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd[ks + 1] + nb * 32 * DP);
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int nb = 0; nb < S::NB; ++nb) sacc[nb] = E::mfma32(a_cur[nb], qreg[ks], sacc[nb]);
+#pragma unroll
+      for (int nb = 0; nb < S::NB; ++nb) a_cur[nb] = a_nxt[nb];
     }
   };
 
@@ -320,6 +332,16 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     for (int cc = 0; cc < S::NC; ++cc) {
       const int nb = cc >> 1;
       const int base = (cc & 1) * 8;
+      // V^T operands of the chunk first: their LDS latency overlaps the exp work
+      u32x4 av[S::DB];
+#pragma unroll
+      for (int db = 0; db < S::DB; ++db) {
+        const uint16_t* r0 = vl + v_rd[db] + 16 * cc * DP;
+        const u32x2 lo2 = lds_read_tr16(r0);             // keys 16cc + 4g + 0..3
+        const u32x2 hi2 = lds_read_tr16(r0 + 8 * DP);    // keys 16cc + 8 + 4g + 0..3
+        av[db] = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
+      }
+      __builtin_amdgcn_sched_barrier(0);
       float pv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -329,13 +351,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
       const u32x4 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]),
                         E::pack2(pv[4], pv[5]), E::pack2(pv[6], pv[7])};
 #pragma unroll
-      for (int db = 0; db < S::DB; ++db) {
-        const uint16_t* r0 = vl + v_rd[db] + 16 * cc * DP;
-        const u32x2 lo2 = lds_read_tr16(r0);             // keys 16cc + 4g + 0..3
-        const u32x2 hi2 = lds_read_tr16(r0 + 8 * DP);    // keys 16cc + 8 + 4g + 0..3
-        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
-        oacc[db] = E::mfma32(a, pk, oacc[db]);
-      }
+      for (int db = 0; db < S::DB; ++db) oacc[db] = E::mfma32(av[db], pk, oacc[db]);
     }
   };
 
