@@ -87,6 +87,23 @@ def blas_threads() -> int:
         return 1
 
 
+PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
+
+
+def profiled_traffic(summary: str):
+    """HBM bytes per launch of a kernel as measured by the committed rocprofv3 PMC
+    summary ``profiles/<summary>`` (line ``traffic_bytes_per_launch: N``: FETCH_SIZE and
+    WRITE_SIZE per dispatch, each scaled by its calibration factor), or None."""
+    try:
+        with open(os.path.join(PROFILES, summary)) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
 def cpu_baseline_prefill(cfg: dict, q, k, v, budget_s: float) -> dict:
     """Oracle restatement of the reference CPU path (numpy, the reference dispatcher's
     block size) over whole (batch 0, head h) slices, h = 0, 1, ... until the time
@@ -160,7 +177,7 @@ def bench_prefill(name: str, steps: int, warmup: int, cpu_budget: float):
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": None,
+            "traffic": profiled_traffic(f"prefill_kernel_{name}.md"),
         },
         "config": {"workload": f"{name}_prefill", "batch": B, "heads_q": Hq, "heads_kv": Hkv,
                    "seq_len": S, "head_dim": D, "causal": cfg["causal"],
@@ -211,7 +228,8 @@ def bench_decode(steps: int, warmup: int):
         "kernel_ms": ms_event,
         "bytes": nbytes,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None},
+                     "frac": achieved / PEAK_HBM_GBS,
+                     "traffic": profiled_traffic("decode_split_kernel_cfg4.md")},
         "config": {"workload": "cfg4_paged_decode", "batch": B, "heads_q": Hq, "heads_kv": Hkv,
                    "head_dim": D, "page_size": P, "context_lens": "U[512, 32768] seed 0",
                    "total_tokens": int(lens.sum())},
@@ -221,19 +239,20 @@ def bench_decode(steps: int, warmup: int):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="north_star", choices=sorted(PREFILL))
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline sample (0 disables it)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
-                    help="run one plain device copy of this many MiB first (a known-size "
-                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+                    help="run one fp32 elementwise kernel over this many MiB first (a "
+                         "known-size kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU; --gpus must be 1 (the hot path "
-              "shards by (batch, head) with no exchange, see DESIGN.md)", file=sys.stderr)
+              "would shard by (batch, head) with no exchange; no multi-GPU figure is "
+              "produced)", file=sys.stderr)
         return 2
 
     import torch

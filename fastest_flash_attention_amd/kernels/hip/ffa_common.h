@@ -123,6 +123,20 @@ __device__ inline void quad_interleave(const u32x4& r0, const u32x4& r1, const u
 
 __device__ inline float wave_xor32(float x) { return __shfl_xor(x, 32); }
 
+// max / sum of x over the lane pair (l, l ^ 32), on the VALU: v_permlane32_swap
+// exchanges the upper half of its first operand with the lower half of its second, so
+// swapping x with itself yields {x[l & 31], x[(l & 31) + 32]} in every lane.
+__device__ inline float wave_pair_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float wave_pair_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // gfx950 data-movement builtins, wrapped in __device__ functions (called from lambdas
 // inside kernels they must not appear in host-side code).
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -131,6 +145,25 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 // global_load_lds_dwordx4: this lane's 16 bytes at `src` land at lds_base + 16 * lane.
 __device__ inline void load_lds16(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_base, 16, 0, 0);
+}
+
+// The same load issued from inline asm, for pipelined tile loads. The compiler does
+// not see an asm load, so it neither counts it nor guards later LDS reads with
+// s_waitcnt vmcnt(0): loads of a future tile stay in flight while the current tile's
+// LDS is read. The caller owns completion (explicit wait_vmcnt before the barrier that
+// publishes the tile) and must not overwrite LDS another wave may still be reading.
+// Address = wave-uniform `base` (SGPR pair) + per-lane 32-bit byte offset `voff`;
+// `lds_base` is the LDS byte address (wave-uniform), carried in M0.
+__device__ inline void load_lds16_async(const void* base, uint32_t voff, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
+               : "memory");
+}
+
+// LDS byte address of a pointer into a __shared__ array (low 32 bits of its flat
+// address are the LDS offset).
+__device__ inline uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lanes 4k..4k+3 point at 16 contiguous

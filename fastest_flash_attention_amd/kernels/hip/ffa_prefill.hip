@@ -314,7 +314,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
 #pragma unroll
       for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[nb][r]);
     }
-    mt = fmaxf(mt, wave_xor32(mt));
+    mt = wave_pair_max(mt);
     const float m_new = fmaxf(m_run, mt);
     const bool need = m_new > m_run + thresh;
     if (__any(need)) {
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     if (i + 1 < nt) step(i + 1, s_nxt, s_cur);
   }
 
-  const float l_tot = l_run + wave_xor32(l_run);
+  const float l_tot = wave_pair_sum(l_run);
   if (wave_live && qrow < p.Sq) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;

@@ -79,4 +79,6 @@ def probe_lib():
     lib.ffa_probe_tr16.argtypes = [ctypes.c_int, ctypes.c_void_p]
     lib.ffa_probe_load_lds.restype = ctypes.c_int
     lib.ffa_probe_load_lds.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.ffa_probe_pair.restype = ctypes.c_int
+    lib.ffa_probe_pair.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
     return lib

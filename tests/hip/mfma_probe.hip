@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "ffa_common.h"
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -92,5 +94,19 @@ extern "C" int ffa_probe_tr16(int mode, void* out) {
 extern "C" int ffa_probe_load_lds(const void* g, void* out) {
   hipLaunchKernelGGL(probe_load_lds, dim3(1), dim3(64), 0, 0, static_cast<const unsigned*>(g),
                      static_cast<unsigned*>(out));
+  return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}
+
+// Lane-pair reductions of the kernels (ffa::wave_pair_max / wave_pair_sum over lanes
+// l and l ^ 32): one wave, 64 inputs, 64 + 64 outputs.
+__global__ void probe_pair(const float* x, float* out) {
+  const int l = threadIdx.x;
+  out[l] = ffa::wave_pair_max(x[l]);
+  out[64 + l] = ffa::wave_pair_sum(x[l]);
+}
+
+extern "C" int ffa_probe_pair(const void* x, void* out) {
+  hipLaunchKernelGGL(probe_pair, dim3(1), dim3(64), 0, 0, static_cast<const float*>(x),
+                     static_cast<float*>(out));
   return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }

@@ -79,3 +79,19 @@ def test_ds_read_tr16_b64_layout(mode):
     addrs = [4 * l if mode == 0 else 64 * (l % 16) + 4 * (l // 16) for l in range(64)]
     window = {a + e for a in addrs for e in range(4)}
     assert set(got.flatten().tolist()) <= window
+
+
+def test_lane_pair_reductions():
+    """wave_pair_max / wave_pair_sum combine lanes l and l ^ 32 (v_permlane32_swap)."""
+    require_gpu()
+    lib = probe_lib()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(64, generator=g, dtype=torch.float32)
+    out = torch.zeros(128, dtype=torch.float32, device="cuda")
+    say("lane pair reduction probe")
+    assert lib.ffa_probe_pair(x.cuda().data_ptr(), out.data_ptr()) == 0
+    got = out.cpu().numpy()
+    xn = x.numpy()
+    partner = xn[np.arange(64) ^ 32]
+    assert np.array_equal(got[:64], np.maximum(xn, partner))
+    assert np.allclose(got[64:], xn + partner, rtol=0, atol=0)
