@@ -154,6 +154,7 @@ int ffa_paged_decode_fwd(const ffa_paged_decode_args* a, void* stream) {
   const size_t need = ffa::decode_workspace_bytes(a->batch, a->heads_q, a->head_dim,
                                                   a->max_context_len, a->tokens_per_split);
   if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need)) return FFA_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 15u) != 0) return FFA_ERR_MISALIGNED;
   return ffa::launch_paged_decode(*a, static_cast<hipStream_t>(stream));
 }
 

@@ -17,6 +17,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -46,6 +47,11 @@ struct Elem<Bf16Tag> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // 16x16x16 MFMA: A lane l = A[l % 16][4(l/16) .. +3], B lane l = B[4(l/16) .. +3][l % 16].
+  __device__ static inline f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                     __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+  }
   // Two fp32 -> packed pair (x in the low half), round to nearest even.
   __device__ static inline uint32_t pack2(float x, float y) {
     f32x2 v = {x, y};
@@ -65,6 +71,10 @@ struct Elem<F16Tag> {
   __device__ static inline f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4 mfma16k16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
   }
   __device__ static inline uint32_t pack2(float x, float y) {
     f32x2 v = {x, y};
@@ -156,6 +166,13 @@ __device__ inline void load_lds16(const void* src, void* lds_base) {
 // `lds_base` is the LDS byte address (wave-uniform), carried in M0.
 __device__ inline void load_lds16_async(const void* base, uint32_t voff, uint32_t lds_base) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
+               : "memory");
+}
+
+// Same, with a per-lane 64-bit address (sources that need not share a 4 GiB window).
+__device__ inline void load_lds16_async(const void* src, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src),
                "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
                : "memory");
 }

@@ -11,17 +11,16 @@
 //                 straight from the pages; every K/V byte is read once and serves all
 //                 G query heads of the group (no repeat_kv). The block-table entries of
 //                 the split are staged in LDS first, so no tile waits on a dependent
-//                 block-table load. Each wave owns every 4th 32-token tile and keeps two
-//                 tiles in flight:
-//                   K  HBM -> registers in MFMA A-operand layout (a lane reads 16 B of
-//                      one token row, 16 lanes cover 16 rows x 64 B);
-//                   V  HBM -> LDS by global_load_lds_dwordx4 (no VGPR staging), rows
-//                      XOR-swizzled, read back transposed by ds_read_b64_tr_b16.
+//                 block-table load. Each wave owns every 4th 16-token tile and keeps a
+//                 2-stage ring in LDS: K and V rows go HBM -> LDS by asm-issued
+//                 global_load_lds_dwordx4 (no VGPR staging, completion tracked by
+//                 explicit vmcnt waits only), XOR-swizzled per row so the K operand
+//                 reads and the transposed V reads are bank-conflict free.
 //                 Per tile: S^T[key, head] = K Q^T (v_mfma_f32_16x16x32), fp32 softmax
-//                 with exp2 and lane swaps (xor 16, 32), rescale deferred until the max
-//                 grows by 2^8, O^T += V^T P^T with P taken straight from the S^T
-//                 accumulators. The 4 waves' partials are merged through LDS and one
-//                 normalised (O, lse) partial per query head goes to the workspace.
+//                 with exp2 and lane swaps, rescale deferred until the max grows by 2^8,
+//                 O^T += V^T P^T (v_mfma_f32_16x16x16) whose B operand is exactly the
+//                 lane's four P values. The waves' partials are merged through LDS and
+//                 one normalised (O, lse) partial per query head goes to the workspace.
 //   combine kernel one wave per (sequence, query head): O = sum_s exp(lse_s - lse) O_s,
 //                 lse = logsumexp_s lse_s.
 // Page ids outside [0, num_pages) read page 0 of the pool's first head instead of
@@ -33,9 +32,9 @@
 namespace ffa {
 namespace {
 
-constexpr int kDecThreads = 256;
 constexpr int kDecWaves = 4;
-constexpr int kTile = 32;            // tokens per wave tile
+constexpr int kDecThreads = 64 * kDecWaves;
+constexpr int kTile = 16;            // tokens per wave tile
 constexpr int kCols = 16;            // query heads per workgroup (MFMA N)
 constexpr int kDefaultSplit = 1024;  // tokens per split
 constexpr int kMaxSplit = 2048;      // bounds the LDS block-table stage
@@ -68,10 +67,6 @@ template <int DP>
 struct DShape {
   static constexpr int KS = DP / 32;          // k-steps of the 16x16x32 QK product
   static constexpr int DB = DP / 16;          // 16-dim blocks of O^T
-  static constexpr int VSTR = DP * 4;         // key-quad row stride (16-bit elements)
-  static constexpr int V_ELEMS = (kTile / 4) * VSTR;  // per wave
-  static constexpr int VITEMS = (kTile / 4) * (DP / 8);
-  static constexpr int VPL = (VITEMS + 63) / 64;      // items per lane
 };
 
 __device__ inline int page_of(const DecodeParams& p, int tok, int& slot) {
@@ -96,20 +91,29 @@ __device__ inline int dec_vswz(int r) {
   return 2 * (r & 7);
 }
 
+// XOR swizzle (16-byte chunk index) of the K rows in LDS: the 16 rows x 16 bytes one
+// K operand read fetches per 16 lanes land in distinct bank groups.
+template <int DP>
+__device__ inline int dec_kswz(int r) {
+  if constexpr (DP == 32) return (r >> 2) & 3;
+  if constexpr (DP == 64 || DP == 192) return (r >> 1) & 7;
+  return r & 15;
+}
+
 template <typename Tag, int DP, bool SOFTCAP>
 __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_kernel(
     const DecodeParams p) {
   using S = DShape<DP>;
   using E = Elem<Tag>;
   constexpr int CPR = DP / 8;                    // 16-byte chunks per row
-  constexpr int VTILE = kTile * DP;              // elements of one V tile
-  constexpr int VLOADS = kTile * CPR / 64;       // V direct loads per lane per tile
-  constexpr int KLOADS = 2 * S::KS;              // K register loads per lane per tile
-  constexpr int NL = VLOADS + KLOADS;            // vector memory ops per lane per tile
-  // V stages (2 per wave) during the sweep; reused for the wave merge afterwards.
-  constexpr int kVBytes = kDecWaves * 2 * VTILE * 2;
+  constexpr int TILE = kTile * DP;               // elements of one K (or V) tile
+  constexpr int NLD = kTile * CPR / 64;          // direct loads per lane per tile, per tensor
+  constexpr int NL = 2 * NLD;                    // vector memory ops per lane per tile
+  static_assert(kTile * CPR % 64 == 0, "tile rows must fill whole wave loads");
+  // Per wave: 2 stages x (K tile, V tile); reused for the wave merge afterwards.
+  constexpr int kStageBytes = kDecWaves * 2 * 2 * TILE * 2;
   constexpr int kRedBytes = kDecWaves * kCols * (DP + 1) * 4;
-  __shared__ __attribute__((aligned(1024))) char smem[kVBytes > kRedBytes ? kVBytes : kRedBytes];
+  __shared__ __attribute__((aligned(1024))) char smem[kStageBytes > kRedBytes ? kStageBytes : kRedBytes];
   __shared__ int bt_lds[kMaxSplit + 2];
   __shared__ float red_m[kDecWaves][kCols];
   __shared__ float red_l[kDecWaves][kCols];
@@ -171,6 +175,10 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
       qreg[ks] = (col_live && 32 * ks + 8 * g4 < D) ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
+  // Every compiler-issued load (block table, Q) is complete before the tile loop: the
+  // tile loads below are asm direct-to-LDS loads whose completion the loop tracks with
+  // explicit vmcnt waits, and no compiler wait inside the loop may count them.
+  wait_vmcnt0();
   __syncthreads();  // bt_lds ready
 
   f32x4 oacc[S::DB];
@@ -180,19 +188,29 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   float l_run = 0.0f;
 
   const int n_tiles = (s_end - s_begin + kTile - 1) / kTile;
-  uint16_t* vstage = reinterpret_cast<uint16_t*>(smem) + wave * 2 * VTILE;
-  u32x4 kreg0[2][S::KS];  // K of the stage-0 tile (registers), stage 1 below
-  u32x4 kreg1[2][S::KS];
+  // stage st of this wave: K tile at kst(st), V tile right after it
+  uint16_t* const wbase = reinterpret_cast<uint16_t*>(smem) + wave * 2 * 2 * TILE;
+  auto kst = [&](int st) { return wbase + st * 2 * TILE; };
+  auto vst = [&](int st) { return wbase + st * 2 * TILE + TILE; };
 
-  // Per-lane constants of the V direct loads: load j fills chunk position
-  // j * 64 + lane of the tile -> row, swizzled source chunk.
-  int vrow[VLOADS];
-  int vchk[VLOADS];
+  // Per-lane constants of the direct loads: load j fills chunk position j * 64 + lane
+  // of a tile -> row, swizzled source chunk (K and V swizzles differ).
+  int lrow[NLD];
+  int kchk[NLD];
+  int vchk[NLD];
 #pragma unroll
-  for (int j = 0; j < VLOADS; ++j) {
+  for (int j = 0; j < NLD; ++j) {
     const int pos = j * 64 + lane;
-    vrow[j] = pos / CPR;
-    vchk[j] = min((pos - vrow[j] * CPR) ^ dec_vswz<DP>(vrow[j]), dchunks - 1);
+    lrow[j] = pos / CPR;
+    const int q = pos - lrow[j] * CPR;
+    kchk[j] = min(q ^ dec_kswz<DP>(lrow[j]), dchunks - 1) * 16;
+    vchk[j] = min(q ^ dec_vswz<DP>(lrow[j]), dchunks - 1) * 16;
+  }
+  // Per-lane K operand addresses: key c16, chunk 4*ks + g4 (dims 32ks + 8g4).
+  int krd[S::KS];
+#pragma unroll
+  for (int ks = 0; ks < S::KS; ++ks) {
+    krd[ks] = c16 * DP + (((4 * ks + g4) ^ dec_kswz<DP>(c16)) << 3);
   }
   // Per-lane V^T operand addresses (elements) of dim block db inside a V tile: this
   // lane supplies row 4*g4 + (c16 >> 2) of a 4-key group and dims 4*(c16 & 3) .. +3
@@ -205,55 +223,47 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
     vrd[db] = vr * DP + (((col >> 3) ^ dec_vswz<DP>(vr)) << 3) + (col & 7);
   }
 
-  auto issue = [&](int it, int st, u32x4 (&kreg)[2][S::KS]) {
+  auto issue = [&](int it, int st) {
     const int t0 = s_begin + it * kTile;
+    uint16_t* kd = kst(st);
+    uint16_t* vd = vst(st);
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const char* row = kpool + row_off(t0 + 16 * sub + c16);
-#pragma unroll
-      for (int ks = 0; ks < S::KS; ++ks) {
-        const int d0 = min(32 * ks + 8 * g4, D - 8);
-        kreg[sub][ks] = *reinterpret_cast<const u32x4*>(row + d0 * 2);
-      }
-    }
-    uint16_t* dst = vstage + st * VTILE;
-#pragma unroll
-    for (int j = 0; j < VLOADS; ++j) {
-      load_lds16(vpool + row_off(t0 + vrow[j]) + vchk[j] * 16, dst + j * 512);
+    for (int j = 0; j < NLD; ++j) {
+      const int64_t ro = row_off(t0 + lrow[j]);
+      load_lds16_async(kpool + ro + kchk[j], lds_addr(kd + j * 512));
+      load_lds16_async(vpool + ro + vchk[j], lds_addr(vd + j * 512));
     }
   };
 
-  auto compute = [&](int it, int st, const u32x4 (&kreg)[2][S::KS]) {
+  // One 16-token tile: S^T[key, head] = K Q^T (v_mfma_f32_16x16x32: lane holds keys
+  // 4*g4 + j of head c16), fp32 softmax, then O^T += V^T P^T with v_mfma_f32_16x16x16:
+  // its B operand (keys 4*g4 .. +3 of head c16) is exactly this lane's four P values.
+  auto compute = [&](int it, int st) {
     const int t0 = s_begin + it * kTile;
-    f32x4 sacc[2];
+    const uint16_t* kl = kst(st);
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      sacc[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < S::KS; ++ks) {
-        // dims >= head_dim of K were clamped re-reads: the zero Q dims cancel them
-        sacc[sub] = E::mfma16(kreg[sub][ks], qreg[ks], sacc[sub]);
-      }
+    for (int ks = 0; ks < S::KS; ++ks) {
+      // dims >= head_dim of K were clamped re-reads: the zero Q dims cancel them
+      const u32x4 a = *reinterpret_cast<const u32x4*>(kl + krd[ks]);
+      sacc = E::mfma16(a, qreg[ks], sacc);
     }
     float mt = kNegInf;
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float x = sacc[sub][j];
-        if constexpr (SOFTCAP) {
-          x = p.cap_mul * tanh_approx(x * p.score_mul);
-        } else {
-          x = x * p.score_mul;
-        }
-        const int tok = t0 + 16 * sub + 4 * g4 + j;
-        x = (tok < s_end) ? x : kNegInf;  // tokens below `lo` never enter a split range
-        sacc[sub][j] = x;
-        mt = fmaxf(mt, x);
+    for (int j = 0; j < 4; ++j) {
+      float x = sacc[j];
+      if constexpr (SOFTCAP) {
+        x = p.cap_mul * tanh_approx(x * p.score_mul);
+      } else {
+        x = x * p.score_mul;
       }
+      const int tok = t0 + 4 * g4 + j;
+      x = (tok < s_end) ? x : kNegInf;  // tokens below `lo` never enter a split range
+      sacc[j] = x;
+      mt = fmaxf(mt, x);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = wave_pair_max(mt);
     const float m_new = fmaxf(m_run, mt);
     const bool need = m_new > m_run + kRescaleThresh;
     if (__any(need)) {
@@ -267,52 +277,45 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
       }
     }
     const float mu = (m_run == kNegInf) ? 0.0f : m_run;
-    float pv[8];
+    float pv[4];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pv[4 * sub + j] = fast_exp2(sacc[sub][j] - mu);
-        l_run += pv[4 * sub + j];
-      }
+    for (int j = 0; j < 4; ++j) {
+      pv[j] = fast_exp2(sacc[j] - mu);
+      l_run += pv[j];
     }
-    const u32x4 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]), E::pack2(pv[4], pv[5]),
-                      E::pack2(pv[6], pv[7])};
-    const uint16_t* vl = vstage + st * VTILE;
+    const u32x2 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3])};
+    const uint16_t* vl = vst(st);
 #pragma unroll
     for (int db = 0; db < S::DB; ++db) {
-      const u32x2 a0 = lds_read_tr16(vl + vrd[db]);            // keys 4*g4 + 0..3
-      const u32x2 a1 = lds_read_tr16(vl + vrd[db] + 16 * DP);  // keys 16 + 4*g4 + 0..3
-      const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
-      oacc[db] = E::mfma16(a, pk, oacc[db]);
+      const u32x2 a = lds_read_tr16(vl + vrd[db]);  // dim 16db + c16, keys 4*g4 + 0..3
+      oacc[db] = E::mfma16k16(a, pk, oacc[db]);
     }
   };
 
-  // Wave w owns tiles w, w + 4, ...; its i-th tile uses stage i & 1 (the loop is
-  // written for both stages so register arrays are never indexed at run time).
-  // Entering the compute of tile i, tiles i and i+1 are in flight: waiting until at
-  // most one tile's NL memory ops remain leaves tile i complete (in-order counter).
+  // Wave w owns tiles w, w + W, ... (W waves); its i-th tile uses stage i & 1. Entering
+  // the compute of tile i, tiles i and i+1 are in flight: waiting until at most one
+  // tile's NL loads remain leaves tile i complete (the counter retires in order).
   const int my_tiles = n_tiles > wave ? (n_tiles - wave + kDecWaves - 1) / kDecWaves : 0;
-  if (my_tiles > 0) issue(wave, 0, kreg0);
-  if (my_tiles > 1) issue(wave + kDecWaves, 1, kreg1);
-  auto step = [&](int i, int st, u32x4 (&kreg)[2][S::KS]) {
+  if (my_tiles > 0) issue(wave, 0);
+  if (my_tiles > 1) issue(wave + kDecWaves, 1);
+  auto step = [&](int i, int st) {
     if (i + 1 < my_tiles) {
       wait_vmcnt<NL>();
     } else {
       wait_vmcnt0();
     }
-    compute(wave + i * kDecWaves, st, kreg);
+    compute(wave + i * kDecWaves, st);
     if (i + 2 < my_tiles) {
-      wait_lgkmcnt0();  // this stage's transposed reads are done before it is refilled
-      issue(wave + (i + 2) * kDecWaves, st, kreg);
+      wait_lgkmcnt0();  // this stage's LDS reads are done before it is refilled
+      issue(wave + (i + 2) * kDecWaves, st);
     }
   };
   for (int i = 0; i < my_tiles; i += 2) {
-    step(i, 0, kreg0);
-    if (i + 1 < my_tiles) step(i + 1, 1, kreg1);
+    step(i, 0);
+    if (i + 1 < my_tiles) step(i + 1, 1);
   }
 
-  // Per-wave totals, then merge the 4 waves through LDS.
+  // Per-wave totals, then merge the waves through LDS.
   float l_w = l_run + __shfl_xor(l_run, 16);
   l_w += __shfl_xor(l_w, 32);
   __syncthreads();  // every wave is done with its V stages
@@ -352,6 +355,10 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   }
 }
 
+// One wave per (sequence, query head): O = sum_s w_s O_s / sum_s w_s with
+// w_s = exp(lse_s - max lse). Lane l owns dims 2l, 2l + 1 of each 128-dim slice, so a
+// split's partial row is one coalesced 512-byte read; splits are walked 8 at a time
+// to keep eight reads in flight per lane.
 template <typename Tag>
 __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p) {
   using E = Elem<Tag>;
@@ -364,31 +371,56 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p
   const int s0 = lo / p.tps;
   const int s1 = L > 0 ? (L + p.tps - 1) / p.tps : 0;
   const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.n_splits;
+  const float* lse_row = p.ws_lse + base;
 
   float mm = kNegInf;
-  for (int s = s0 + lane; s < s1; s += 64) mm = fmaxf(mm, p.ws_lse[base + s]);
+  for (int s = s0 + lane; s < s1; s += 64) mm = fmaxf(mm, lse_row[s]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mm = fmaxf(mm, __shfl_xor(mm, off));
 
   float wsum = 0.0f;
   if (mm != kNegInf) {
-    for (int s = s0 + lane; s < s1; s += 64) wsum += __expf(p.ws_lse[base + s] - mm);
+    for (int s = s0 + lane; s < s1; s += 64) wsum += __expf(lse_row[s] - mm);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) wsum += __shfl_xor(wsum, off);
+  const float inv = (mm != kNegInf && wsum > 0.0f) ? 1.0f / wsum : 0.0f;
 
   uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh;
-  for (int d = lane; d < p.D; d += 64) {
-    float acc = 0.0f;
+  const bool o_pair_aligned = (reinterpret_cast<uintptr_t>(orow) & 3u) == 0;
+  for (int d0 = 2 * lane; d0 < p.D; d0 += 128) {
+    f32x2 acc = {0.0f, 0.0f};
     if (mm != kNegInf) {
-      for (int s = s0; s < s1; ++s) {
-        const float ls = p.ws_lse[base + s];
-        if (ls != kNegInf) acc += __expf(ls - mm) * p.ws_o[(base + s) * p.dp + d];
+      const float* col = p.ws_o + base * p.dp + d0;
+      int s = s0;
+      for (; s + 8 <= s1; s += 8) {
+        f32x2 v[8];
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          v[u] = *reinterpret_cast<const f32x2*>(col + static_cast<int64_t>(s + u) * p.dp);
+          w[u] = __expf(lse_row[s + u] - mm);  // exp(-inf) = 0 for empty partials
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          acc[0] += w[u] * v[u][0];
+          acc[1] += w[u] * v[u][1];
+        }
       }
-      acc = acc / wsum;
+      for (; s < s1; ++s) {
+        const f32x2 v = *reinterpret_cast<const f32x2*>(col + static_cast<int64_t>(s) * p.dp);
+        const float w = __expf(lse_row[s] - mm);
+        acc[0] += w * v[0];
+        acc[1] += w * v[1];
+      }
     }
-    const uint32_t w = E::pack2(acc, 0.0f);
-    orow[d] = static_cast<uint16_t>(w & 0xffffu);
+    const uint32_t pr = E::pack2(acc[0] * inv, acc[1] * inv);
+    if (d0 + 1 < p.D && o_pair_aligned) {
+      *reinterpret_cast<uint32_t*>(orow + d0) = pr;
+    } else {
+      orow[d0] = static_cast<uint16_t>(pr & 0xffffu);
+      if (d0 + 1 < p.D) orow[d0 + 1] = static_cast<uint16_t>(pr >> 16);
+    }
   }
   if (lane == 0 && p.lse != nullptr) {
     p.lse[b * p.l_sb + hq * p.l_sh] = (mm != kNegInf && wsum > 0.0f) ? mm + logf(wsum) : kNegInf;
@@ -455,8 +487,6 @@ void launch_decode_tag(DecodeParams& p, bool softcap, dim3 grid, hipStream_t s) 
 }
 
 int dp_of(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : d <= 192 ? 192 : 256; }
-
-bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 }  // namespace
 

@@ -29,11 +29,12 @@ from ..kernels import _lib
 
 
 def _auto_tokens_per_split(batch: int, heads_kv: int, max_len: int) -> int:
-    """Largest split (<= 2048 tokens, >= 64) that still yields >= 1024 workgroups, so
-    small batches keep all 256 CUs streaming while long contexts amortise each
-    workgroup's pipeline fill."""
-    tps = 2048
-    while tps > 64 and batch * heads_kv * max(1, math.ceil(max_len / tps)) < 1024:
+    """Largest split (<= 512 tokens, >= 64) that still yields >= 2048 workgroups. Many
+    short splits keep the tail of the grid short on 256 CUs (two workgroups each);
+    512 tokens (8 tiles per wave) was the fastest split on MI355X for the long-context
+    batch of the decode benchmark (B=64, 8 KV heads, lengths up to 32k)."""
+    tps = 512
+    while tps > 64 and batch * heads_kv * max(1, math.ceil(max_len / tps)) < 2048:
         tps //= 2
     return tps
 

@@ -144,9 +144,10 @@ int ffa_paged_gather(const ffa_paged_gather_args* args, void* stream);
  *   q   : [batch, heads_q, head_dim] (strides q_stride[b, h], dim stride 1)
  *   o   : [batch, heads_q, head_dim] (strides o_stride[b, h])
  *   lse : [batch, heads_q] fp32 (strides lse_stride[b, h]) or NULL
- * context_lens[b] == 0 gives O = 0 and lse = -inf. head_dim % 8 == 0; q and the pools
- * are 16-byte aligned and q's strides are multiples of 8 (FFA_ERR_MISALIGNED).
- * tokens_per_split is rounded up to a multiple of 32 and clamped to [32, 2048].
+ * context_lens[b] == 0 gives O = 0 and lse = -inf. head_dim % 8 == 0; q, the pools and
+ * the workspace are 16-byte aligned and q's strides are multiples of 8
+ * (FFA_ERR_MISALIGNED). tokens_per_split is rounded up to a multiple of 16 and clamped
+ * to [32, 2048].
  * Split-K: each sequence is cut into chunks of tokens_per_split tokens processed
  * by independent workgroups; partials (O, lse) go to the caller's workspace and
  * are merged by logsumexp weights.

@@ -110,3 +110,28 @@ extern "C" int ffa_probe_pair(const void* x, void* out) {
                      static_cast<float*>(out));
   return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }
+
+// v_mfma_f32_16x16x16bf16_1k: A lane l = A[l%16][4(l/16)..+3], B lane l =
+// B[4(l/16)..+3][l%16], acc[j] = C[4(l/16)+j][l%16] (A, B 16x16, out 64x4).
+__global__ void probe16k16(const uint16_t* A, const uint16_t* B, float* out) {
+  const int l = threadIdx.x;
+  ffa::u32x2 a, b;
+  uint16_t av[4], bv[4];
+  for (int e = 0; e < 4; ++e) {
+    av[e] = A[(l % 16) * 16 + 4 * (l / 16) + e];
+    bv[e] = B[(4 * (l / 16) + e) * 16 + l % 16];
+  }
+  a[0] = av[0] | (uint32_t(av[1]) << 16);
+  a[1] = av[2] | (uint32_t(av[3]) << 16);
+  b[0] = bv[0] | (uint32_t(bv[1]) << 16);
+  b[1] = bv[2] | (uint32_t(bv[3]) << 16);
+  ffa::f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  c = ffa::Elem<ffa::Bf16Tag>::mfma16k16(a, b, c);
+  for (int j = 0; j < 4; ++j) out[l * 4 + j] = c[j];
+}
+
+extern "C" int ffa_probe_mfma16k16(const void* A, const void* B, void* out) {
+  hipLaunchKernelGGL(probe16k16, dim3(1), dim3(64), 0, 0, static_cast<const uint16_t*>(A),
+                     static_cast<const uint16_t*>(B), static_cast<float*>(out));
+  return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}

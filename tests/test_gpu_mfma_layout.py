@@ -48,6 +48,21 @@ def test_mfma_16x16x32_layout():
             assert got[lane, j] == C[4 * (lane // 16) + j, lane % 16], (lane, j)
 
 
+def test_mfma_16x16x16_layout():
+    require_gpu()
+    lib = probe_lib()
+    A = _small_ints((16, 16), 6)
+    B = _small_ints((16, 16), 7)
+    C = (A.double() @ B.double()).numpy()
+    out = torch.zeros(64, 4, dtype=torch.float32, device="cuda")
+    say("mfma 16x16x16 layout probe")
+    assert lib.ffa_probe_mfma16k16(A.cuda().data_ptr(), B.cuda().data_ptr(), out.data_ptr()) == 0
+    got = out.cpu().numpy()
+    for lane in range(64):
+        for j in range(4):
+            assert got[lane, j] == C[4 * (lane // 16) + j, lane % 16], (lane, j)
+
+
 def test_global_load_lds_lane_placement():
     """global_load_lds_dwordx4: lane l's 16 bytes land at LDS base + 16 l."""
     require_gpu()

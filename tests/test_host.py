@@ -194,6 +194,7 @@ def test_workspace_sizing(lib):
     assert lib.ffa_paged_decode_num_splits(32768, 512) == 64
     assert lib.ffa_paged_decode_num_splits(1000, 0) == 1  # default split 1024
     assert lib.ffa_paged_decode_num_splits(5000, 4096) == 3  # split clamped to 2048
+    assert lib.ffa_paged_decode_num_splits(100, 40) == 3  # 40 rounds up to 48 (16-token tiles)
     assert lib.ffa_paged_decode_workspace_bytes(64, 32, 128, 32768, 512) == 64 * 32 * 64 * 129 * 4
     assert lib.ffa_paged_decode_workspace_bytes(2, 4, 100, 100, 64) == 2 * 4 * 2 * 129 * 4
 
@@ -241,3 +242,11 @@ def test_paged_cache_out_of_pages_matches_reference_state():
         pool.append_tokens(0, k.numpy(), k.numpy())
     assert cache.sequences == pool.sequences and cache.free_pages == pool.free_pages
     assert np.array_equal(cache.k_pages.numpy(), pool.k_pages)
+
+
+def test_auto_tokens_per_split():
+    from fastest_flash_attention_amd.ops.kv_cache import _auto_tokens_per_split
+
+    assert _auto_tokens_per_split(64, 8, 32768) == 512   # long-context batch: 512-token splits
+    assert _auto_tokens_per_split(1, 8, 4096) == 64       # small batch: shortest split
+    assert _auto_tokens_per_split(4, 8, 8192) == 128      # 4*8*64 = 2048 workgroups
