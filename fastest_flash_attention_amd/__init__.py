@@ -9,8 +9,13 @@ libffa.so (C ABI: include/ffa.h).
 from .config import AttentionConfig
 from .modules import FastestFlashGQA, FastestFlashMHA, FastestFlashMLA
 from .ops import (
+    ContinuousKVCache,
     FastestFlashAttnFunc,
     PagedKVCache,
+    combine_block_masks,
+    create_causal_block_mask,
+    create_local_block_mask,
+    create_sliding_window_block_mask,
     fastest_flash_attn_forward,
     fastest_flash_attn_func,
     fastest_flash_paged_decode,
@@ -29,6 +34,11 @@ __all__ = [
     "FastestFlashGQA",
     "FastestFlashMLA",
     "PagedKVCache",
+    "ContinuousKVCache",
+    "create_causal_block_mask",
+    "create_sliding_window_block_mask",
+    "create_local_block_mask",
+    "combine_block_masks",
     "auto_select_block_size",
     "check_hip_available",
     "check_triton_available",

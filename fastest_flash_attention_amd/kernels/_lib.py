@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime before libffa.so)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libffa.so")
 
-FFA_ABI_VERSION = 1
+FFA_ABI_VERSION = 2
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
 
@@ -58,6 +58,9 @@ class PrefillArgs(ctypes.Structure):
         ("ref_block_kv", ctypes.c_int32),
         ("masked_lse_mode", ctypes.c_int32),
         ("dtype", ctypes.c_int32),
+        ("block_key_mask", ctypes.c_void_p),
+        ("block_key_mask_words", ctypes.c_int32),
+        ("block_visited", ctypes.c_void_p),
     ]
 
 
@@ -75,6 +78,27 @@ class PagedGatherArgs(ctypes.Structure):
         ("page_size", ctypes.c_int32),
         ("head_dim", ctypes.c_int32),
         ("context_len", ctypes.c_int32),
+        ("elem_bytes", ctypes.c_int32),
+    ]
+
+
+class PagedAppendArgs(ctypes.Structure):
+    """Mirror of ``ffa_paged_append_args``."""
+
+    _fields_ = [
+        ("k_pages", ctypes.c_void_p),
+        ("v_pages", ctypes.c_void_p),
+        ("k_new", ctypes.c_void_p),
+        ("v_new", ctypes.c_void_p),
+        ("page_table", ctypes.c_void_p),
+        ("k_new_stride", _I64x2),
+        ("v_new_stride", _I64x2),
+        ("num_pages", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("start", ctypes.c_int32),
+        ("n_tokens", ctypes.c_int32),
         ("elem_bytes", ctypes.c_int32),
     ]
 
@@ -115,6 +139,7 @@ class PagedDecodeArgs(ctypes.Structure):
 EXPORTS = {
     "ffa_prefill_fwd": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]),
     "ffa_paged_gather": (ctypes.c_int, [ctypes.POINTER(PagedGatherArgs), ctypes.c_void_p]),
+    "ffa_paged_append": (ctypes.c_int, [ctypes.POINTER(PagedAppendArgs), ctypes.c_void_p]),
     "ffa_paged_decode_num_splits": (ctypes.c_int32, [ctypes.c_int32, ctypes.c_int32]),
     "ffa_paged_decode_workspace_bytes": (
         ctypes.c_size_t,

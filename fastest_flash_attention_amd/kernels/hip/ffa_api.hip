@@ -81,6 +81,13 @@ int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
       if (st[i] % 8 != 0) return FFA_ERR_MISALIGNED;
     }
   }
+  if (a->block_key_mask != nullptr) {
+    const int64_t need_words = (static_cast<int64_t>(a->seqlen_kv) + 63) / 64;
+    if (a->block_visited == nullptr || a->block_key_mask_words < need_words ||
+        a->ref_block_q <= 0 || (reinterpret_cast<uintptr_t>(a->block_key_mask) & 7u) != 0) {
+      return FFA_ERR_INVALID_ARG;
+    }
+  }
   // per-tile byte offsets of K/V rows are 32-bit
   if (a->k_stride[2] >= (int64_t{1} << 24) || a->v_stride[2] >= (int64_t{1} << 24)) {
     return FFA_ERR_TOO_LARGE;
@@ -106,6 +113,25 @@ int ffa_paged_gather(const ffa_paged_gather_args* a, void* stream) {
     return FFA_ERR_INVALID_ARG;
   }
   return ffa::launch_paged_gather(*a, static_cast<hipStream_t>(stream));
+}
+
+int ffa_paged_append(const ffa_paged_append_args* a, void* stream) {
+  if (a == nullptr) return FFA_ERR_INVALID_ARG;
+  if (a->elem_bytes != 2 && a->elem_bytes != 4) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (a->heads_kv < 1 || a->page_size < 1 || a->head_dim < 1 || a->n_tokens < 0 ||
+      a->start < 0 || a->num_pages < 1) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->n_tokens == 0) return FFA_OK;
+  if (a->k_pages == nullptr || a->v_pages == nullptr || a->k_new == nullptr ||
+      a->v_new == nullptr || a->page_table == nullptr) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  for (int i = 0; i < 2; ++i) {
+    if (a->k_new_stride[i] < 0 || a->v_new_stride[i] < 0) return FFA_ERR_INVALID_ARG;
+  }
+  if (static_cast<int64_t>(a->start) + a->n_tokens > 0x7fffffff) return FFA_ERR_TOO_LARGE;
+  return ffa::launch_paged_append(*a, static_cast<hipStream_t>(stream));
 }
 
 int32_t ffa_paged_decode_num_splits(int32_t max_context_len, int32_t tokens_per_split) {

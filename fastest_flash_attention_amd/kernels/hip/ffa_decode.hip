@@ -456,6 +456,32 @@ __global__ __launch_bounds__(256) void paged_gather_kernel(const U* __restrict__
   }
 }
 
+// append_tokens: token t (0 <= t < n) of [H, n, D] new K/V goes to page
+// pt[(start + t) / P], slot (start + t) % P of every head. One thread per unit U of
+// a row; consecutive threads cover consecutive units of one (head, token) row, so the
+// reads of a row and its write into the page are both contiguous.
+template <typename U>
+__global__ __launch_bounds__(256) void paged_append_kernel(
+    U* __restrict__ kp, U* __restrict__ vp, const U* __restrict__ kn, const U* __restrict__ vn,
+    const int32_t* __restrict__ pt, int64_t k_sh, int64_t k_st, int64_t v_sh, int64_t v_st,
+    int num_pages, int H, int P, int row_units, int start, int n) {
+  const int64_t total = static_cast<int64_t>(H) * n * row_units;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int u = static_cast<int>(i % row_units);
+    const int64_t ht = i / row_units;
+    const int t = static_cast<int>(ht % n);
+    const int h = static_cast<int>(ht / n);
+    const int pos = start + t;
+    const int phys = pt[pos / P];
+    if (phys < 0 || phys >= num_pages) continue;
+    const int slot = pos - (pos / P) * P;
+    const int64_t dst = ((static_cast<int64_t>(phys) * H + h) * P + slot) * row_units + u;
+    kp[dst] = kn[h * k_sh + t * k_st + u];
+    vp[dst] = vn[h * v_sh + t * v_st + u];
+  }
+}
+
 template <typename Tag, int DP>
 void launch_decode_dp(const DecodeParams& p, bool softcap, dim3 grid, hipStream_t s) {
   if (softcap) {
@@ -597,6 +623,50 @@ int launch_paged_gather(const ffa_paged_gather_args& a, hipStream_t stream) {
                        static_cast<const uint16_t*>(a.v_pages), static_cast<uint16_t*>(a.k_out),
                        static_cast<uint16_t*>(a.v_out), a.page_table, a.num_pages, a.heads_kv,
                        a.page_size, ru, a.context_len);
+  }
+  return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
+}
+
+int launch_paged_append(const ffa_paged_append_args& a, hipStream_t stream) {
+  const int64_t row_bytes = static_cast<int64_t>(a.head_dim) * a.elem_bytes;
+  const uintptr_t align = reinterpret_cast<uintptr_t>(a.k_pages) |
+                          reinterpret_cast<uintptr_t>(a.v_pages) |
+                          reinterpret_cast<uintptr_t>(a.k_new) |
+                          reinterpret_cast<uintptr_t>(a.v_new);
+  // strides in bytes must keep every row on the unit's alignment
+  const int64_t sb[4] = {a.k_new_stride[0] * a.elem_bytes, a.k_new_stride[1] * a.elem_bytes,
+                         a.v_new_stride[0] * a.elem_bytes, a.v_new_stride[1] * a.elem_bytes};
+  auto fits = [&](int64_t unit) {
+    if (row_bytes % unit != 0 || (align % unit) != 0) return false;
+    for (int64_t x : sb) {
+      if (x % unit != 0) return false;
+    }
+    return true;
+  };
+  const int64_t rows = static_cast<int64_t>(a.heads_kv) * a.n_tokens;
+  auto grid_for = [&](int64_t units) {
+    const int64_t blocks = (units + 255) / 256;
+    return static_cast<unsigned>(blocks < 65536 ? (blocks < 1 ? 1 : blocks) : 65536);
+  };
+  auto run = [&](auto unit_tag, int64_t unit) {
+    using U = decltype(unit_tag);
+    const int ru = static_cast<int>(row_bytes / unit);
+    const int64_t eu = unit / a.elem_bytes;  // elements per unit
+    hipLaunchKernelGGL(paged_append_kernel<U>, dim3(grid_for(rows * ru)), dim3(256), 0, stream,
+                       static_cast<U*>(a.k_pages), static_cast<U*>(a.v_pages),
+                       static_cast<const U*>(a.k_new), static_cast<const U*>(a.v_new),
+                       a.page_table, a.k_new_stride[0] / eu, a.k_new_stride[1] / eu,
+                       a.v_new_stride[0] / eu, a.v_new_stride[1] / eu, a.num_pages, a.heads_kv,
+                       a.page_size, ru, a.start, a.n_tokens);
+  };
+  if (fits(16)) {
+    run(u32x4{}, 16);
+  } else if (fits(4)) {
+    run(uint32_t{}, 4);
+  } else if (a.elem_bytes == 2) {
+    run(uint16_t{}, 2);
+  } else {
+    return FFA_ERR_MISALIGNED;  // 4-byte elements off 4-byte alignment
   }
   return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
 }

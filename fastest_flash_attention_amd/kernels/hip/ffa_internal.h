@@ -20,5 +20,6 @@ int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream);
 
 // get_kv gather.
 int launch_paged_gather(const ffa_paged_gather_args& a, hipStream_t stream);
+int launch_paged_append(const ffa_paged_append_args& a, hipStream_t stream);
 
 }  // namespace ffa

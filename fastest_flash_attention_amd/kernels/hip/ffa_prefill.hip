@@ -59,6 +59,9 @@ struct PrefillParams {
   int ref_bq, ref_bkv;
   int masked_lse_mode;
   int xcd_remap;
+  const uint64_t* kmask;  // block mask expanded to keys, [n_br][kmask_words], or null
+  int kmask_words;
+  const int32_t* visited;  // reference tiles visited per row block (with kmask)
 };
 
 template <int DP, int BN>
@@ -95,6 +98,10 @@ __device__ inline int vswz(int r) {
 // (ref_bq x ref_bkv) tiles, visited per cpu_reference.py:215-231.
 __device__ float masked_row_lse(const PrefillParams& p, int row) {
   if (p.masked_lse_mode != 0) return kNegInf;
+  if (p.kmask != nullptr) {
+    const int n = p.visited[row / p.ref_bq];
+    return n > 0 ? logf(static_cast<float>(n)) + logf(1e-30f) : kNegInf;
+  }
   const int bq = p.ref_bq;
   const int bkv = p.ref_bkv;
   const int iq = row / bq;
@@ -169,6 +176,10 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   const int qw0_abs = p.q_offset + qw0;
   const int qwl_abs = p.q_offset + min(qw0 + 31, p.Sq - 1);
   const int qa = p.q_offset + qrow;
+  // block mask: this lane's row block in the expanded key mask
+  const uint64_t* kmask_row =
+      p.kmask != nullptr ? p.kmask + static_cast<int64_t>(min(qrow, p.Sq - 1) / p.ref_bq) * p.kmask_words
+                         : nullptr;
 
   // Scores stay in raw (q.k) units until the exponent: p = exp2(s*c - m*c).
   const float c = SOFTCAP ? 1.0f : p.score_mul;
@@ -295,15 +306,20 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
       }
     }
     const bool need_mask = (kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
-                           (p.window > 0 && kt0 < qwl_abs - p.window + 1);
+                           (p.window > 0 && kt0 < qwl_abs - p.window + 1) ||
+                           kmask_row != nullptr;
     if (need_mask) {
+      // keys kt0 .. kt0 + BN - 1 of the block mask (BN divides 64, kt0 % BN == 0)
+      const uint64_t kbits =
+          kmask_row != nullptr ? kmask_row[kt0 >> 6] >> (kt0 & 63) : ~uint64_t{0};
 #pragma unroll
       for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = kt0 + 32 * nb + 8 * (r >> 2) + 4 * g + (r & 3);
+          const int off = 32 * nb + 8 * (r >> 2) + 4 * g + (r & 3);
+          const int key = kt0 + off;
           const bool ok = key < Skv && (!p.causal || key <= qa) &&
-                          (p.window <= 0 || key >= qa - p.window + 1);
+                          (p.window <= 0 || key >= qa - p.window + 1) && ((kbits >> off) & 1u);
           sacc[nb][r] = ok ? sacc[nb][r] : kNegInf;
         }
       }
@@ -479,6 +495,9 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   p.ref_bq = a.ref_block_q > 0 ? a.ref_block_q : 64;
   p.ref_bkv = a.ref_block_kv > 0 ? a.ref_block_kv : 64;
   p.masked_lse_mode = a.masked_lse_mode;
+  p.kmask = a.block_key_mask;
+  p.kmask_words = a.block_key_mask_words;
+  p.visited = a.block_visited;
 
   // The kernels move 16-byte chunks: callers guarantee 16-byte aligned bases, strides
   // that are multiples of 8 elements and head_dim % 8 == 0 (checked by ffa_prefill_fwd),

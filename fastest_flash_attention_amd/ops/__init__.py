@@ -1,13 +1,25 @@
-"""Ops layer: the forward entry point, the autograd wrapper and the paged KV cache."""
+"""Ops layer: the forward entry point, the autograd wrapper, block-sparse masks and
+the KV caches."""
 
 from .attention_forward import fastest_flash_attn_forward
 from .attention_func import FastestFlashAttnFunc, fastest_flash_attn_func
-from .kv_cache import PagedKVCache, fastest_flash_paged_decode
+from .block_sparse import (
+    combine_block_masks,
+    create_causal_block_mask,
+    create_local_block_mask,
+    create_sliding_window_block_mask,
+)
+from .kv_cache import ContinuousKVCache, PagedKVCache, fastest_flash_paged_decode
 
 __all__ = [
     "fastest_flash_attn_forward",
     "FastestFlashAttnFunc",
     "fastest_flash_attn_func",
+    "ContinuousKVCache",
     "PagedKVCache",
     "fastest_flash_paged_decode",
+    "create_causal_block_mask",
+    "create_sliding_window_block_mask",
+    "create_local_block_mask",
+    "combine_block_masks",
 ]

@@ -67,6 +67,44 @@ class PrefillCall:
     lse: Optional[torch.Tensor]
     squeezed: bool
     d_user: int = 0
+    keep: tuple = ()  # device buffers the launch reads (block-mask words, counts)
+
+
+def _expand_block_mask(block_mask, r: "ResolvedForward", device) -> Tuple[torch.Tensor, int, torch.Tensor]:
+    """The reference's ``[n_br, n_bc]`` tile mask (cpu_reference.py:220-222) in the form
+    the kernel reads: per query tile i, bit k of the 64-bit word array = mask[i][k //
+    block_kv] (keys >= S_kv clear), plus the number of tiles the reference loop visits
+    per query tile (mask set, not past the causal bound, not left of the window;
+    cpu_reference.py:215-231), which fixes the LSE sentinel of rows with no visible
+    key. All on the device."""
+    bq, bkv = r.block_q, r.block_kv
+    n_br = math.ceil(r.S_q / bq)
+    n_bc = math.ceil(r.S_kv / bkv) if r.S_kv > 0 else 0
+    bm = torch.as_tensor(block_mask)
+    if bm.dim() != 2 or bm.shape[0] < n_br or bm.shape[1] < n_bc:
+        raise ValueError(f"block_mask of shape {tuple(bm.shape)} does not cover the "
+                         f"[{n_br}, {n_bc}] tiles of block size ({bq}, {bkv})")
+    bm = bm[:n_br, :n_bc].to(device=device, dtype=torch.bool)
+    words = max(1, math.ceil(r.S_kv / 64))
+    keys = torch.arange(words * 64, device=device)
+    if n_bc > 0:
+        bits = bm[:, torch.clamp(keys // bkv, max=n_bc - 1)] & (keys < r.S_kv)[None, :]
+    else:
+        bits = torch.zeros(n_br, words * 64, dtype=torch.bool, device=device)
+    shifts = torch.arange(64, device=device, dtype=torch.int64)
+    packed = (bits.view(n_br, words, 64).to(torch.int64) << shifts).sum(dim=-1).contiguous()
+    i = torch.arange(n_br, device=device)
+    j = torch.arange(n_bc, device=device)
+    visit = bm.clone()
+    if r.causal:
+        q_last = r.q_offset + torch.clamp((i + 1) * bq, max=r.S_q) - 1
+        visit &= (j * bkv)[None, :] <= q_last[:, None]
+    if r.sliding_window is not None:
+        q_first = r.q_offset + i * bq
+        k_last = torch.clamp((j + 1) * bkv, max=r.S_kv) - 1
+        visit &= k_last[None, :] >= (q_first - r.sliding_window + 1)[:, None]
+    visited = visit.sum(dim=1).to(torch.int32).contiguous()
+    return packed, words, visited
 
 
 def _conform(t: torch.Tensor, d_pad: int) -> torch.Tensor:
@@ -213,15 +251,6 @@ def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> Pref
     """Resolve arguments, check device/dtype/features, allocate outputs, build the ABI
     struct. Launches nothing."""
     r = resolve_forward_args(*args, **kwargs)
-    if r.block_mask is not None:
-        raise NotImplementedError(
-            "fastest_flash_attention_amd: block_mask is not supported by the HIP kernel yet"
-        )
-    if r.compute_dtype is not None and r.compute_dtype != r.q.dtype:
-        raise NotImplementedError(
-            "fastest_flash_attention_amd: compute_dtype different from the input dtype is "
-            "not supported by the HIP kernel yet"
-        )
     for name, t in (("q", r.q), ("k", r.k), ("v", r.v)):
         if t.device.type != "cuda":
             raise RuntimeError(
@@ -233,6 +262,16 @@ def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> Pref
     if not (r.q.dtype == r.k.dtype == r.v.dtype):
         raise TypeError(f"q/k/v dtypes differ: {r.q.dtype}, {r.k.dtype}, {r.v.dtype}")
     code = _lib.dtype_code(r.q.dtype)
+    if r.compute_dtype is not None and r.compute_dtype != r.q.dtype:
+        # The reference rounds q and k (not v) to compute_dtype before the fp32 product
+        # (cpu_reference.py:260-262). fp32 is exact for 16-bit inputs; a 16-bit compute
+        # dtype is applied as an exact round trip q -> compute_dtype -> q.dtype (every
+        # bf16/fp16 value of the rounded tensor is representable in the input dtype).
+        if r.compute_dtype in (torch.bfloat16, torch.float16):
+            r.q = r.q.to(r.compute_dtype).to(r.q.dtype)
+            r.k = r.k.to(r.compute_dtype).to(r.k.dtype)
+        elif r.compute_dtype != torch.float32:
+            raise TypeError(f"unsupported compute_dtype {r.compute_dtype}")
     if r.D > 256:
         raise ValueError(f"head_dim {r.D} > 256 is not supported")
     d_pad = (r.D + 7) // 8 * 8
@@ -251,6 +290,12 @@ def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> Pref
     call = PrefillCall(build_prefill_args(r, out, lse, code), r.q, r.k, r.v, out, lse,
                        r.squeezed)
     call.d_user = d_user
+    if r.block_mask is not None:
+        packed, words, visited = _expand_block_mask(r.block_mask, r, r.q.device)
+        call.args.block_key_mask = packed.data_ptr()
+        call.args.block_key_mask_words = words
+        call.args.block_visited = visited.data_ptr()
+        call.keep = (packed, visited)
     return call
 
 

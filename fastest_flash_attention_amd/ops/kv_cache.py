@@ -166,6 +166,73 @@ def fastest_flash_paged_decode(
     return out, lse
 
 
+class ContinuousKVCache:
+    """Contiguous KV-cache appended in place (reference ops/kv_cache.py:18-107).
+
+    Buffers ``k_cache`` / ``v_cache`` are ``[max_batch, num_heads, max_seq_len,
+    head_dim]`` zeros; ``seq_lens`` (int64, on ``device``) holds each entry's length and
+    is the source of truth, as in the reference. ``append`` writes every batch entry's
+    new block with one scatter (the reference loops over the batch).
+    """
+
+    def __init__(
+        self,
+        max_batch: int,
+        max_seq_len: int,
+        num_heads: int,
+        head_dim: int,
+        dtype: torch.dtype = torch.float16,
+        device: torch.device | str = "cpu",
+    ):
+        self.max_batch = max_batch
+        self.max_seq_len = max_seq_len
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.k_cache = torch.zeros(max_batch, num_heads, max_seq_len, head_dim,
+                                   dtype=dtype, device=device)
+        self.v_cache = torch.zeros(max_batch, num_heads, max_seq_len, head_dim,
+                                   dtype=dtype, device=device)
+        self.seq_lens = torch.zeros(max_batch, dtype=torch.long, device=device)
+
+    def reset(self, batch_indices: Optional[torch.Tensor] = None):
+        """Reset all entries, or the indexed ones (reference :61-66)."""
+        if batch_indices is None:
+            self.seq_lens.zero_()
+        else:
+            self.seq_lens[batch_indices] = 0
+
+    def append(self, k_new: torch.Tensor, v_new: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Append ``[B, H, S_new, D]`` K/V at each entry's current length and return the
+        cached ``[B, H, max_len, D]`` views (reference :68-97). On overflow the entries
+        before the first overflowing one are written and advanced, then AssertionError
+        is raised, as in the reference loop."""
+        B, H, S_new, D = k_new.shape
+        starts = self.seq_lens[:B].tolist()
+        fail = next((b for b in range(B) if starts[b] + S_new > self.max_seq_len), B)
+        dev = self.k_cache.device
+        if S_new > 0 and fail > 0:
+            pos = (torch.tensor(starts[:fail], dtype=torch.int64).unsqueeze(1)
+                   + torch.arange(S_new, dtype=torch.int64).unsqueeze(0)).to(dev)
+            bidx = torch.arange(fail, device=dev).unsqueeze(1).expand(fail, S_new)
+            dt = self.k_cache.dtype
+            self.k_cache[bidx, :, pos, :] = k_new[:fail].to(dev, dt).permute(0, 2, 1, 3)
+            self.v_cache[bidx, :, pos, :] = v_new[:fail].to(dev, dt).permute(0, 2, 1, 3)
+        self.seq_lens[:fail] += S_new
+        if fail < B:
+            end = starts[fail] + S_new
+            raise AssertionError(f"KV-cache overflow: {end} > {self.max_seq_len}")
+        max_len = max(starts) + S_new if B > 0 else 0
+        return self.k_cache[:B, :, :max_len, :], self.v_cache[:B, :, :max_len, :]
+
+    def get_cache(self, batch_size: int) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+        """Cached ``[batch_size, H, max_len, D]`` views, or ``(None, None)`` when empty
+        (reference :99-107)."""
+        max_len = int(self.seq_lens[:batch_size].max().item()) if batch_size > 0 else 0
+        if max_len == 0:
+            return None, None
+        return self.k_cache[:batch_size, :, :max_len, :], self.v_cache[:batch_size, :, :max_len, :]
+
+
 class PagedKVCache:
     """Paged KV-cache (vLLM-style page tables), reference ops/kv_cache.py:110-240.
 
@@ -236,17 +303,50 @@ class PagedKVCache:
         n_fit = min(S_new, len(seq["page_table"]) * P - L0)
         if n_fit > 0:
             dev = self.k_pages.device
-            t = torch.arange(L0, L0 + n_fit, dtype=torch.int64)
-            table = torch.tensor(seq["page_table"], dtype=torch.int64)
-            phys = table[t // P].to(dev)
-            slot = (t % P).to(dev)
             dt = self.k_pages.dtype  # slice assignment in the reference casts implicitly
-            self.k_pages[phys, :, slot, :] = k_tokens[:, :n_fit, :].transpose(0, 1).to(dev, dt)
-            self.v_pages[phys, :, slot, :] = v_tokens[:, :n_fit, :].transpose(0, 1).to(dev, dt)
+            kn = k_tokens[:, :n_fit, :].to(dev, dt)
+            vn = v_tokens[:, :n_fit, :].to(dev, dt)
+            if dev.type == "cuda":
+                self._append_device(seq, L0, kn, vn)
+            else:
+                t = torch.arange(L0, L0 + n_fit, dtype=torch.int64)
+                table = torch.tensor(seq["page_table"], dtype=torch.int64)
+                phys, slot = table[t // P], t % P
+                self.k_pages[phys, :, slot, :] = kn.transpose(0, 1)
+                self.v_pages[phys, :, slot, :] = vn.transpose(0, 1)
             seq["len"] = L0 + n_fit
         if out_of_pages:
             raise RuntimeError("PagedKVCache: out of physical pages")
         return seq["len"]
+
+    def _append_device(self, seq: dict, start: int, kn: torch.Tensor, vn: torch.Tensor) -> None:
+        """One ``ffa_paged_append`` launch: scatter [H, n, D] new rows into the pages."""
+        if kn.stride(-1) != 1:
+            kn = kn.contiguous()
+        if vn.stride(-1) != 1:
+            vn = vn.contiguous()
+        table = torch.tensor(seq["page_table"], dtype=torch.int32, device=self.k_pages.device)
+        a = _lib.PagedAppendArgs()
+        a.k_pages = self.k_pages.data_ptr()
+        a.v_pages = self.v_pages.data_ptr()
+        a.k_new = kn.data_ptr()
+        a.v_new = vn.data_ptr()
+        a.page_table = table.data_ptr()
+        a.k_new_stride[:] = [kn.stride(0), kn.stride(1)]
+        a.v_new_stride[:] = [vn.stride(0), vn.stride(1)]
+        a.num_pages = self.max_pages
+        a.heads_kv = self.num_heads
+        a.page_size = self.page_size
+        a.head_dim = self.head_dim
+        a.start = start
+        a.n_tokens = kn.size(1)
+        a.elem_bytes = self.k_pages.element_size()
+        if a.elem_bytes not in (2, 4):
+            raise TypeError(f"PagedKVCache: pool dtype {self.k_pages.dtype} is not supported on the GPU")
+        lib = _lib.load()
+        with torch.cuda.device(self.k_pages.device):
+            stream = _lib.current_stream_handle(self.k_pages.device)
+            _lib.check(lib.ffa_paged_append(ctypes.byref(a), ctypes.c_void_p(stream)))
 
     def _page_table_tensor(self, seq_id: int) -> torch.Tensor:
         return torch.tensor(self.sequences[seq_id]["page_table"], dtype=torch.int32,

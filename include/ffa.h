@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FFA_ABI_VERSION 1
+#define FFA_ABI_VERSION 2
 
 typedef enum ffa_status {
   FFA_OK = 0,
@@ -71,6 +71,11 @@ typedef enum ffa_dtype {
  *            log(n * 1e-30), n = number of (ref_block_q x ref_block_kv) tiles the
  *            reference loop visits for that row (-inf when n == 0, and always -inf
  *            with masked_lse_mode = 1).
+ * Block sparsity (the reference's block_mask, cpu_reference.py:220-222): when
+ * block_key_mask is not NULL, key k is also masked for row r unless bit (k % 64) of
+ * block_key_mask[(r / ref_block_q) * block_key_mask_words + k / 64] is set (the
+ * [n_br, n_bc] tile mask expanded to keys: bit k of row-block i = block_mask[i][k /
+ * ref_block_kv]); block_visited[r / ref_block_q] then gives the sentinel's n.
  * GQA: q head h reads kv head h / (heads_q / heads_kv)  (utils.py:111-130).
  * Layout: element strides per tensor in order [batch, head, seq, dim]; the dim
  * stride must be 1. A batch or head stride may be 0 (broadcast). lse strides are
@@ -105,6 +110,10 @@ typedef struct ffa_prefill_args {
   int32_t masked_lse_mode;  /* 0: one-pass sentinel log(n*1e-30); 1: -inf (the
                                reference's two_pass LSE, cpu_reference.py:63-125) */
   int32_t dtype;            /* ffa_dtype */
+  const uint64_t* block_key_mask;  /* NULL: no block mask; else [n_br][words] bits */
+  int32_t block_key_mask_words;    /* words per row block, >= ceil(seqlen_kv / 64) */
+  const int32_t* block_visited;    /* [n_br] reference tiles visited per row block
+                                      (required with block_key_mask) */
 } ffa_prefill_args;
 
 int ffa_prefill_fwd(const ffa_prefill_args* args, void* stream);
@@ -132,6 +141,35 @@ typedef struct ffa_paged_gather_args {
 } ffa_paged_gather_args;
 
 int ffa_paged_gather(const ffa_paged_gather_args* args, void* stream);
+
+/*
+ * Append n_tokens new tokens to one sequence (PagedKVCache.append_tokens,
+ * ops/kv_cache.py:170-206): token t of the new block is token start + t of the
+ * sequence and goes to page page_table[(start + t) / page_size], slot
+ * (start + t) % page_size, for every KV head. The caller has allocated the pages
+ * (page_table holds >= ceil((start + n_tokens) / page_size) valid ids, each in
+ * [0, num_pages); FFA_ERR_INVALID_ARG is not detected on the device for bad ids,
+ * which are skipped). k_new / v_new are [heads_kv, n_tokens, head_dim] with element
+ * strides new_stride[head, token] (dim stride 1) and the pool's dtype.
+ */
+typedef struct ffa_paged_append_args {
+  void* k_pages;
+  void* v_pages;
+  const void* k_new;
+  const void* v_new;
+  const int32_t* page_table;  /* device, the sequence's page table */
+  int64_t k_new_stride[2];
+  int64_t v_new_stride[2];
+  int32_t num_pages;
+  int32_t heads_kv;
+  int32_t page_size;
+  int32_t head_dim;
+  int32_t start;              /* tokens already stored for the sequence */
+  int32_t n_tokens;
+  int32_t elem_bytes;         /* 2 or 4 */
+} ffa_paged_append_args;
+
+int ffa_paged_append(const ffa_paged_append_args* args, void* stream);
 
 /*
  * Batched paged decode: one query token per sequence, attending to the first

@@ -8,6 +8,8 @@ Modules (each cites the reference file:line it restates):
   reference_forward  flash_attn_cpu_forward + dispatcher CPU branch (numpy fp32)
   naive              fp64 brute-force masked SDPA (pins reference_forward)
   paged              PagedKVCache index law, get_kv gather, decode oracle
+  block_masks        block-sparse mask generators, tiles visited per query tile
+  caches             ContinuousKVCache
 
 Parity pinning status (tests/test_oracle.py): every function above is pinned; see
 the module docstrings for what pins each.

@@ -154,8 +154,12 @@ def test_rejects_unsupported():
     with pytest.raises(TypeError):
         ffa.fastest_flash_attn_forward(q, q, q)
     qb = q.to(BF16)
-    with pytest.raises(NotImplementedError):
-        ffa.fastest_flash_attn_forward(qb, qb, qb, block_mask=torch.ones(1, 1, dtype=torch.bool))
+    with pytest.raises(ValueError, match="does not cover"):
+        # 8 rows / block 4 = 2 query tiles: a 1x1 mask is too small
+        ffa.fastest_flash_attn_forward(qb, qb, qb, block_size=4,
+                                       block_mask=torch.ones(1, 1, dtype=torch.bool))
+    with pytest.raises(TypeError, match="compute_dtype"):
+        ffa.fastest_flash_attn_forward(qb, qb, qb, compute_dtype=torch.int8)
 
 
 # ---------------------------------------------------------------------------------

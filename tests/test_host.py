@@ -100,8 +100,10 @@ def test_product_path_refuses_cpu_and_unsupported():
     q = torch.randn(1, 1, 8, 16, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
         ffa.fastest_flash_attn_forward(q, q, q)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
         af.prepare_prefill(q, q, q, block_mask=torch.ones(1, 1, dtype=torch.bool))
+    with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
+        af.prepare_prefill(q, q, q, compute_dtype=torch.float16)
     cache = ffa.PagedKVCache(max_pages=4, page_size=4, num_heads=1, head_dim=8)
     cache.append_tokens(0, torch.randn(1, 3, 8), torch.randn(1, 3, 8))
     with pytest.raises(RuntimeError, match="ROCm"):
@@ -147,6 +149,7 @@ def _c_layout(struct: str, fields: list[str]) -> dict:
     (_lib.PrefillArgs, "ffa_prefill_args"),
     (_lib.PagedGatherArgs, "ffa_paged_gather_args"),
     (_lib.PagedDecodeArgs, "ffa_paged_decode_args"),
+    (_lib.PagedAppendArgs, "ffa_paged_append_args"),
 ])
 def test_ctypes_struct_matches_header(cls, cname):
     fields = [f for f, _ in cls._fields_]
