@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libffa.so")
 FFA_ABI_VERSION = 2
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
+FFA_DTYPE_FP32 = 2
 
 _I64x4 = ctypes.c_int64 * 4
 _I64x3 = ctypes.c_int64 * 3
@@ -202,14 +203,17 @@ def strerror(rc: int) -> str:
     return load().ffa_strerror(rc).decode()
 
 
-def dtype_code(dtype: torch.dtype) -> int:
+def dtype_code(dtype: torch.dtype, allow_fp32: bool = False) -> int:
+    """ABI dtype code; float32 only where the entry point has an fp32 kernel (prefill)."""
     if dtype == torch.bfloat16:
         return FFA_DTYPE_BF16
     if dtype == torch.float16:
         return FFA_DTYPE_FP16
+    if dtype == torch.float32 and allow_fp32:
+        return FFA_DTYPE_FP32
     raise TypeError(
-        f"fastest_flash_attention_amd: dtype {dtype} is not supported by the HIP kernels "
-        "(bfloat16, float16)"
+        f"fastest_flash_attention_amd: dtype {dtype} is not supported by this HIP kernel "
+        f"(bfloat16, float16{', float32' if allow_fp32 else ''})"
     )
 
 

@@ -26,7 +26,7 @@ const char* ffa_strerror(int status) {
     case FFA_ERR_INVALID_ARG:
       return "ffa: invalid argument (null pointer, non-positive size or bad stride)";
     case FFA_ERR_UNSUPPORTED_DTYPE:
-      return "ffa: unsupported dtype (bfloat16 and float16 are supported)";
+      return "ffa: unsupported dtype (bfloat16 and float16; float32 for prefill)";
     case FFA_ERR_UNSUPPORTED_HEAD_DIM:
       return "ffa: unsupported head_dim (1..256 supported)";
     case FFA_ERR_MISALIGNED:
@@ -49,7 +49,7 @@ const char* ffa_strerror(int status) {
 
 int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
   if (a == nullptr) return FFA_ERR_INVALID_ARG;
-  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (!valid_dtype(a->dtype) && a->dtype != FFA_DTYPE_FP32) return FFA_ERR_UNSUPPORTED_DTYPE;
   if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
   if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->seqlen_q < 0 || a->seqlen_kv < 0) {
     return FFA_ERR_INVALID_ARG;

@@ -447,7 +447,223 @@ void launch_tag(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
   }
 }
 
-bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+// ---------------------------------------------------------------------------------
+// fp32 inputs: the reference computes them in fp32 (cpu_reference.py:262), so they run
+// on v_mfma_f32_32x32x2_f32 instead of being rounded to 16 bits. One workgroup of 4
+// waves per 128 query rows, 32-key tiles of K and V staged in LDS (rows padded by 4
+// floats: the K operand reads of 32 rows and the V reads of 32 dims are conflict
+// free). S^T = K Q^T with the reduction dims permuted per lane half (k-step ks: dim ks
+// for lanes 0-31, DP/2 + ks for lanes 32-63) so every lane's Q and K operands are
+// contiguous. For O^T += V^T P^T the keys are permuted so that k-step (i, j) covers
+// keys 8i + j and 8i + 4 + j: each lane's B operand is then its own S^T accumulator
+// 4i + j (fp32 P, no shuffle).
+// ---------------------------------------------------------------------------------
+constexpr int kF32BN = 32;
+
+__device__ inline f32x16 mfma_f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillParams p) {
+  constexpr int PITCH = DP + 4;
+  constexpr int HALF = DP / 2;
+  constexpr int DB = DP / 32;
+  __shared__ __attribute__((aligned(16))) float kt[kF32BN * PITCH];
+  __shared__ __attribute__((aligned(16))) float vt[kF32BN * PITCH];
+  const float* qf = reinterpret_cast<const float*>(p.q);
+  const float* kf = reinterpret_cast<const float*>(p.k);
+  const float* vf = reinterpret_cast<const float*>(p.v);
+  float* of = reinterpret_cast<float*>(p.o);
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  int bid = blockIdx.x;
+  if (p.xcd_remap) {
+    const int per_xcd = gridDim.x >> 3;
+    bid = (bid & 7) * per_xcd + (bid >> 3);
+  }
+  const int bh = bid / p.n_qt;
+  const int jq = bid - bh * p.n_qt;
+  const int qt = p.causal ? (p.n_qt - 1 - jq) : jq;
+  const int b = bh / p.Hq;
+  const int h = bh - b * p.Hq;
+  const int hk = h / p.ratio;
+  const int D = p.D;
+  const int Skv = p.Skv;
+
+  const int q0 = qt * kBlockM;
+  const int q_last = min(q0 + kBlockM, p.Sq) - 1;
+  const int q0_abs = p.q_offset + q0;
+  const int ql_abs = p.q_offset + q_last;
+  const int kv_lo = p.window > 0 ? max(0, q0_abs - p.window + 1) : 0;
+  const int kv_hi = p.causal ? min(Skv, ql_abs + 1) : Skv;
+  const int t_begin = kv_lo / kF32BN;
+  const int nt = kv_hi > kv_lo ? (kv_hi + kF32BN - 1) / kF32BN - t_begin : 0;
+
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + l32;
+  const bool wave_live = qw0 < p.Sq;
+  const int qw0_abs = p.q_offset + qw0;
+  const int qwl_abs = p.q_offset + min(qw0 + 31, p.Sq - 1);
+  const int qa = p.q_offset + qrow;
+  const uint64_t* kmask_row =
+      p.kmask != nullptr ? p.kmask + static_cast<int64_t>(min(qrow, p.Sq - 1) / p.ref_bq) * p.kmask_words
+                         : nullptr;
+  const float c = SOFTCAP ? 1.0f : p.score_mul;
+  const float thresh = SOFTCAP ? kRescaleThresh : kRescaleThresh / p.score_mul;
+
+  // Q^T operand: lane holds row qrow, dims g*HALF .. g*HALF + HALF - 1 (zero past D)
+  float qreg[HALF];
+  {
+    const float* qr = qf + b * p.q_sb + h * p.q_sh + static_cast<int64_t>(min(qrow, p.Sq - 1)) * p.q_ss;
+#pragma unroll
+    for (int c4 = 0; c4 < HALF; c4 += 4) {
+      const int d0 = g * HALF + c4;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (d0 < D) v = *reinterpret_cast<const f32x4*>(qr + d0);  // D % 8 == 0
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qreg[c4 + e] = v[e];
+    }
+  }
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
+  }
+  float m_run = kNegInf;
+  float l_run = 0.0f;
+  const float* kbase = kf + b * p.k_sb + hk * p.k_sh;
+  const float* vbase = vf + b * p.v_sb + hk * p.v_sh;
+  const int dq = D >> 2;  // float4 chunks per row
+
+  for (int i = 0; i < nt; ++i) {
+    const int kt0 = (t_begin + i) * kF32BN;
+    __syncthreads();  // previous tile's reads are done
+    for (int idx = tid; idx < kF32BN * (DP / 4); idx += kThreads) {
+      const int r = idx / (DP / 4);
+      const int c4 = idx - r * (DP / 4);
+      const int key = min(kt0 + r, Skv - 1);  // rows past Skv are masked below
+      f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+      if (c4 < dq) {
+        kv = *reinterpret_cast<const f32x4*>(kbase + static_cast<int64_t>(key) * p.k_ss + 4 * c4);
+        vv = *reinterpret_cast<const f32x4*>(vbase + static_cast<int64_t>(key) * p.v_ss + 4 * c4);
+      }
+      *reinterpret_cast<f32x4*>(kt + r * PITCH + 4 * c4) = kv;
+      *reinterpret_cast<f32x4*>(vt + r * PITCH + 4 * c4) = vv;
+    }
+    __syncthreads();
+    if (!wave_live) continue;
+    if (p.causal && kt0 > qwl_abs) continue;  // past this wave's causal band
+
+    f32x16 sacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+    const float* krow = kt + l32 * PITCH + g * HALF;
+#pragma unroll
+    for (int ks = 0; ks < HALF; ++ks) sacc = mfma_f32(krow[ks], qreg[ks], sacc);
+
+    if constexpr (SOFTCAP) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = p.cap_mul * tanh_approx(sacc[r] * p.score_mul);
+    }
+    const bool need_mask = (kt0 + kF32BN > Skv) || (p.causal && kt0 + kF32BN - 1 > qw0_abs) ||
+                           (p.window > 0 && kt0 < qwl_abs - p.window + 1) || kmask_row != nullptr;
+    if (need_mask) {
+      const uint64_t kbits =
+          kmask_row != nullptr ? kmask_row[kt0 >> 6] >> (kt0 & 63) : ~uint64_t{0};
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int off = 8 * (r >> 2) + 4 * g + (r & 3);
+        const int key = kt0 + off;
+        const bool ok = key < Skv && (!p.causal || key <= qa) &&
+                        (p.window <= 0 || key >= qa - p.window + 1) && ((kbits >> off) & 1u);
+        sacc[r] = ok ? sacc[r] : kNegInf;
+      }
+    }
+    float mt = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[r]);
+    mt = wave_pair_max(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const bool need = m_new > m_run + thresh;
+    if (__any(need)) {
+      const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
+      m_run = need ? m_new : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      }
+    }
+    const float mc = (m_run == kNegInf) ? 0.0f : m_run * c;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = fast_exp2(fmaf(sacc[r], c, -mc));
+      l_run += sacc[r];
+    }
+    // O^T[d, q] += sum over keys 8ii + 4g + jj of V[key][d] P[q][key]
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r >> 2) + 4 * g + (r & 3);
+        oacc[db] = mfma_f32(vt[key * PITCH + 32 * db + l32], sacc[r], oacc[db]);
+      }
+    }
+  }
+
+  const float l_tot = wave_pair_sum(l_run);
+  if (wave_live && qrow < p.Sq) {
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    float* orow = of + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int d0 = 32 * db + 8 * ii + 4 * g;
+        const f32x4 w = {oacc[db][4 * ii + 0] * inv, oacc[db][4 * ii + 1] * inv,
+                         oacc[db][4 * ii + 2] * inv, oacc[db][4 * ii + 3] * inv};
+        if (d0 < D) *reinterpret_cast<f32x4*>(orow + d0) = w;
+      }
+    }
+    if (p.lse != nullptr && g == 0) {
+      const float lse = l_tot > 0.0f ? (m_run * c + fast_log2(l_tot)) * kLn2
+                                     : masked_row_lse(p, qrow);
+      p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(qrow) * p.l_ss] = lse;
+    }
+  }
+}
+
+template <int DP>
+void launch_f32_dp(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
+  if (softcap) {
+    hipLaunchKernelGGL((prefill_f32_kernel<DP, true>), dim3(grid), dim3(kThreads), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((prefill_f32_kernel<DP, false>), dim3(grid), dim3(kThreads), 0, s, p);
+  }
+}
+
+void launch_f32(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
+  if (p.D <= 32) {
+    launch_f32_dp<32>(p, softcap, grid, s);
+  } else if (p.D <= 64) {
+    launch_f32_dp<64>(p, softcap, grid, s);
+  } else if (p.D <= 128) {
+    launch_f32_dp<128>(p, softcap, grid, s);
+  } else if (p.D <= 192) {
+    launch_f32_dp<192>(p, softcap, grid, s);
+  } else {
+    launch_f32_dp<256>(p, softcap, grid, s);
+  }
+}
+
 
 }  // namespace
 
@@ -510,8 +726,10 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
 
   if (a.dtype == FFA_DTYPE_BF16) {
     launch_tag<Bf16Tag>(p, softcap, grid, stream);
-  } else {
+  } else if (a.dtype == FFA_DTYPE_FP16) {
     launch_tag<F16Tag>(p, softcap, grid, stream);
+  } else {
+    launch_f32(p, softcap, grid, stream);
   }
   return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
 }

@@ -261,12 +261,14 @@ def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> Pref
         raise RuntimeError("q, k, v must be on the same device")
     if not (r.q.dtype == r.k.dtype == r.v.dtype):
         raise TypeError(f"q/k/v dtypes differ: {r.q.dtype}, {r.k.dtype}, {r.v.dtype}")
-    code = _lib.dtype_code(r.q.dtype)
+    code = _lib.dtype_code(r.q.dtype, allow_fp32=True)
     if r.compute_dtype is not None and r.compute_dtype != r.q.dtype:
         # The reference rounds q and k (not v) to compute_dtype before the fp32 product
         # (cpu_reference.py:260-262). fp32 is exact for 16-bit inputs; a 16-bit compute
         # dtype is applied as an exact round trip q -> compute_dtype -> q.dtype (every
         # bf16/fp16 value of the rounded tensor is representable in the input dtype).
+        # fp32 inputs with a 16-bit compute dtype take the same round trip (the values
+        # stay fp32, rounded as the reference rounds them).
         if r.compute_dtype in (torch.bfloat16, torch.float16):
             r.q = r.q.to(r.compute_dtype).to(r.q.dtype)
             r.k = r.k.to(r.compute_dtype).to(r.k.dtype)

@@ -53,7 +53,8 @@ typedef enum ffa_status {
 
 typedef enum ffa_dtype {
   FFA_DTYPE_BF16 = 0,
-  FFA_DTYPE_FP16 = 1
+  FFA_DTYPE_FP16 = 1,
+  FFA_DTYPE_FP32 = 2   /* ffa_prefill_fwd only: fp32 MFMA, fp32 output */
 } ffa_dtype;
 
 /*
@@ -79,7 +80,8 @@ typedef enum ffa_dtype {
  * GQA: q head h reads kv head h / (heads_q / heads_kv)  (utils.py:111-130).
  * Layout: element strides per tensor in order [batch, head, seq, dim]; the dim
  * stride must be 1. A batch or head stride may be 0 (broadcast). lse strides are
- * [batch, head, seq]. q/k/v/o share the dtype. q/k/v/o are 16-byte aligned, head_dim
+ * [batch, head, seq]. q/k/v/o share the dtype (bf16 / fp16 on bf16 / fp16 MFMA with
+ * fp32 softmax and accumulation; fp32 on fp32 MFMA). q/k/v/o are 16-byte aligned, head_dim
  * and the batch/head/seq strides are multiples of 8 elements (FFA_ERR_MISALIGNED
  * otherwise), and k/v seq strides are below 2^24 elements.
  */

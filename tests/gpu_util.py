@@ -72,7 +72,8 @@ def probe_lib():
     if not os.path.exists(PROBE_LIB):
         pytest.skip("tests/hip/libffa_probe.so not built (run __graft_entry__.build())")
     lib = ctypes.CDLL(PROBE_LIB)
-    for name in ("ffa_probe_mfma32", "ffa_probe_mfma16", "ffa_probe_mfma16k16"):
+    for name in ("ffa_probe_mfma32", "ffa_probe_mfma16", "ffa_probe_mfma16k16",
+                 "ffa_probe_mfma32f32"):
         getattr(lib, name).restype = ctypes.c_int
         getattr(lib, name).argtypes = [ctypes.c_void_p] * 3
     lib.ffa_probe_tr16.restype = ctypes.c_int

@@ -135,3 +135,20 @@ extern "C" int ffa_probe_mfma16k16(const void* A, const void* B, void* out) {
                      static_cast<const uint16_t*>(B), static_cast<float*>(out));
   return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
 }
+
+// v_mfma_f32_32x32x2_f32: A lane l = A[l%32][l/32], B lane l = B[l/32][l%32],
+// acc[4i+j] = C[8i+4(l/32)+j][l%32] (A 32x2, B 2x32 fp32, out 64x16).
+__global__ void probe32f32(const float* A, const float* B, float* out) {
+  const int l = threadIdx.x;
+  ffa::f32x16 c;
+  for (int r = 0; r < 16; ++r) c[r] = 0.0f;
+  c = __builtin_amdgcn_mfma_f32_32x32x2f32(A[(l % 32) * 2 + l / 32], B[(l / 32) * 32 + l % 32], c,
+                                           0, 0, 0);
+  for (int r = 0; r < 16; ++r) out[l * 16 + r] = c[r];
+}
+
+extern "C" int ffa_probe_mfma32f32(const void* A, const void* B, void* out) {
+  hipLaunchKernelGGL(probe32f32, dim3(1), dim3(64), 0, 0, static_cast<const float*>(A),
+                     static_cast<const float*>(B), static_cast<float*>(out));
+  return hipDeviceSynchronize() == hipSuccess ? 0 : -1;
+}

@@ -63,6 +63,24 @@ def test_mfma_16x16x16_layout():
             assert got[lane, j] == C[4 * (lane // 16) + j, lane % 16], (lane, j)
 
 
+def test_mfma_32x32x2_f32_layout():
+    require_gpu()
+    lib = probe_lib()
+    g = torch.Generator().manual_seed(8)
+    A = torch.randint(-4, 5, (32, 2), generator=g).float()
+    B = torch.randint(-4, 5, (2, 32), generator=g).float()
+    C = (A.double() @ B.double()).numpy()
+    out = torch.zeros(64, 16, dtype=torch.float32, device="cuda")
+    say("mfma 32x32x2 f32 layout probe")
+    assert lib.ffa_probe_mfma32f32(A.cuda().data_ptr(), B.cuda().data_ptr(), out.data_ptr()) == 0
+    got = out.cpu().numpy()
+    for lane in range(64):
+        g2 = lane // 32
+        for i in range(4):
+            for j in range(4):
+                assert got[lane, 4 * i + j] == C[8 * i + 4 * g2 + j, lane % 32], (lane, i, j)
+
+
 def test_global_load_lds_lane_placement():
     """global_load_lds_dwordx4: lane l's 16 bytes land at LDS base + 16 l."""
     require_gpu()

@@ -152,7 +152,8 @@ def test_rejects_unsupported():
     require_gpu()
     q = torch.randn(1, 1, 8, 16, device="cuda")
     with pytest.raises(TypeError):
-        ffa.fastest_flash_attn_forward(q, q, q)
+        qd = q.double()
+        ffa.fastest_flash_attn_forward(qd, qd, qd)
     qb = q.to(BF16)
     with pytest.raises(ValueError, match="does not cover"):
         # 8 rows / block 4 = 2 query tiles: a 1x1 mask is too small
@@ -203,3 +204,31 @@ def test_full_size_sampled_heads(cfg):
     o0 = o[:, :, 0].float()
     v0 = v[:, torch.arange(Hq, device="cuda") // ratio, 0].float()
     assert (o0 - v0).abs().max().item() < 1e-2
+
+
+# fp32 inputs: computed in fp32 (fp32 MFMA), as the reference computes them; the
+# tolerance is the north-star one, the fp32 path lands far inside it.
+F32_CASES = [
+    ("cfg1_mha_fp32", 2, 8, 8, 1024, 1024, 64, {"causal": True, "block_size": 64}),
+    ("fp32_window_softcap_gqa", 1, 4, 2, 200, 200, 128, {"causal": True, "sliding_window": 50,
+                                                         "softcap": 30.0, "num_kv_heads": 2}),
+    ("fp32_d32_noncausal_rect", 2, 2, 2, 70, 130, 32, {}),
+    ("fp32_d192_masked_rows", 1, 2, 2, 40, 12, 192, {"sliding_window": 5, "block_size": 8}),
+    ("fp32_d256", 1, 2, 2, 66, 66, 256, {"causal": True}),
+]
+
+
+@pytest.mark.parametrize("case", F32_CASES, ids=[c[0] for c in F32_CASES])
+def test_prefill_fp32_parity(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, D, kw = case
+    q = seeded((B, Hq, Sq, D), torch.float32, 51)
+    k = seeded((B, Hkv, Skv, D), torch.float32, 52)
+    v = seeded((B, Hkv, Skv, D), torch.float32, 53)
+    say(f"prefill fp32 {name} B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} {kw}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), return_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float32 and o.shape == q.shape
+    ro, rl = rf.forward(np32(q), np32(k), np32(v), return_lse=True, **kw)
+    max_abs, _ = assert_parity(o, ro, lse, rl, name)
+    assert max_abs < 1e-4, f"{name}: fp32 path max-abs {max_abs:.2e}"
