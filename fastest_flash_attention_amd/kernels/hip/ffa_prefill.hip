@@ -202,6 +202,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     k_off[j] = static_cast<uint32_t>(row * p.k_ss * 2 + kc * 16);
     v_off[j] = static_cast<uint32_t>(row * p.v_ss * 2 + vc * 16);
   }
+  // The loads are issued from inline asm (wave-uniform tile base + 32-bit lane offset):
+  // the compiler neither holds a 64-bit address per load nor guards later LDS reads
+  // with vmcnt waits; completion is the explicit wait_vmcnt0 before each tile barrier.
   auto issue_tile = [&](const char* base, int64_t stride, const uint32_t (&off)[S::LPT],
                         uint16_t* dst, int t) {
     const int kt0 = t * BN;
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     if (kt0 + BN <= Skv) {
 #pragma unroll
       for (int j = 0; j < S::LPT; ++j) {
-        load_lds16(tb + off[j], dst + (4 * j + wave) * 512);
+        load_lds16_async(tb, off[j], lds_addr(dst + (4 * j + wave) * 512));
       }
     } else {
       // last tile: rows past Skv re-read row Skv-1 (their scores are masked to -inf)
@@ -217,8 +220,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
       for (int j = 0; j < S::LPT; ++j) {
         const int row = ((4 * j + wave) * 64 + lane) / S::CPR;
         const int over = max(0, kt0 + row - (Skv - 1));
-        const int64_t back = static_cast<int64_t>(over) * stride * 2;
-        load_lds16(tb + off[j] - back, dst + (4 * j + wave) * 512);
+        const uint32_t back = static_cast<uint32_t>(over * stride * 2);
+        load_lds16_async(tb, off[j] - back, lds_addr(dst + (4 * j + wave) * 512));
       }
     }
   };
@@ -310,14 +313,17 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
                            kmask_row != nullptr;
     if (need_mask) {
       // keys kt0 .. kt0 + BN - 1 of the block mask (BN divides 64, kt0 % BN == 0)
+      // pre-shifted by this lane half's key offset 4g, so each element tests a bit at
+      // a compile-time position (no per-element 64-bit shift constants to hold)
       const uint64_t kbits =
-          kmask_row != nullptr ? kmask_row[kt0 >> 6] >> (kt0 & 63) : ~uint64_t{0};
+          kmask_row != nullptr ? kmask_row[kt0 >> 6] >> ((kt0 & 63) + 4 * g) : ~uint64_t{0};
+      const int key0 = kt0 + 4 * g;
 #pragma unroll
       for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int off = 32 * nb + 8 * (r >> 2) + 4 * g + (r & 3);
-          const int key = kt0 + off;
+          const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
+          const int key = key0 + off;
           const bool ok = key < Skv && (!p.causal || key <= qa) &&
                           (p.window <= 0 || key >= qa - p.window + 1) && ((kbits >> off) & 1u);
           sacc[nb][r] = ok ? sacc[nb][r] : kNegInf;
