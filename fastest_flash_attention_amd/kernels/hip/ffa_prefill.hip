@@ -31,39 +31,15 @@
 
 #include "ffa_common.h"
 #include "ffa_internal.h"
+#include "ffa_prefill_common.h"
 
 namespace ffa {
 namespace {
 
+using namespace pf;
+
 constexpr int kThreads = 256;
 constexpr int kBlockM = 128;
-constexpr float kRescaleThresh = 8.0f;  // log2 units
-
-struct PrefillParams {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  uint16_t* o;
-  float* lse;
-  int64_t q_sb, q_sh, q_ss;
-  int64_t k_sb, k_sh, k_ss;
-  int64_t v_sb, v_sh, v_ss;
-  int64_t o_sb, o_sh, o_ss;
-  int64_t l_sb, l_sh, l_ss;
-  int B, Hq, Hkv, Sq, Skv, D;
-  int q_offset, causal, window;
-  int ratio;
-  int n_qt;
-  float score_mul;  // scale*log2e, or scale/softcap with softcap
-  float cap_mul;    // softcap*log2e (softcap only)
-  int ref_bq, ref_bkv;
-  int masked_lse_mode;
-  int xcd_remap;
-  const uint64_t* kmask;  // block mask expanded to keys, [n_br][kmask_words], or null
-  int kmask_words;
-  const int32_t* visited;  // reference tiles visited per row block (with kmask)
-};
-
 template <int DP, int BN>
 struct Shape {
   static constexpr int CPR = DP / 8;            // 16-byte chunks per row
@@ -75,55 +51,6 @@ struct Shape {
   static constexpr int DB = DP / 32;
   static_assert(BN * CPR % kThreads == 0, "tile must split evenly over the workgroup");
 };
-
-// Row swizzles (XOR on the 16-byte chunk index) of the K and V tiles in LDS. They make
-// the 16 rows read together by a K operand load, and the 4 rows x 64 bytes read
-// together by a transposed V load, land in distinct bank groups.
-template <int DP>
-__device__ inline int kswz(int r) {
-  if constexpr (DP == 32) return (r >> 2) & 3;
-  if constexpr (DP == 64 || DP == 192) return (r >> 1) & 7;
-  return r & 15;
-}
-template <int DP>
-__device__ inline int vswz(int r) {
-  if constexpr (DP == 32) return 0;
-  if constexpr (DP == 64 || DP == 192) return 4 * ((r >> 1) & 1);
-  return 4 * (r & 3);
-}
-
-// LSE of a row with no visible key, as the reference loop produces it: each visited
-// tile adds log(1e-30) by logaddexp (cpu_reference.py:288-297), so n visited tiles
-// give log(n) + log(1e-30); no visited tile leaves -inf. Tiles are the reference's
-// (ref_bq x ref_bkv) tiles, visited per cpu_reference.py:215-231.
-__device__ float masked_row_lse(const PrefillParams& p, int row) {
-  if (p.masked_lse_mode != 0) return kNegInf;
-  if (p.kmask != nullptr) {
-    const int n = p.visited[row / p.ref_bq];
-    return n > 0 ? logf(static_cast<float>(n)) + logf(1e-30f) : kNegInf;
-  }
-  const int bq = p.ref_bq;
-  const int bkv = p.ref_bkv;
-  const int iq = row / bq;
-  const int qs_abs = p.q_offset + iq * bq;
-  const int qe_abs = p.q_offset + min((iq + 1) * bq, p.Sq);
-  const int n_bc = (p.Skv + bkv - 1) / bkv;
-  int j_hi = n_bc - 1;
-  if (p.causal) {
-    const int last = qe_abs - 1;
-    j_hi = last < 0 ? -1 : min(j_hi, last / bkv);
-  }
-  int j_lo = 0;
-  if (p.window > 0) {
-    const int thr = qs_abs - p.window + 1;
-    int j = (thr + 1 <= 0) ? 0 : (thr + bkv) / bkv - 1;
-    if (j >= n_bc - 1) j = (p.Skv - 1 >= thr) ? n_bc - 1 : n_bc;
-    j_lo = j;
-  }
-  const int n = j_hi - j_lo + 1;
-  if (n <= 0) return kNegInf;
-  return logf(static_cast<float>(n)) + logf(1e-30f);
-}
 
 // Two workgroups per CU (2 waves per SIMD, <= 256 VGPRs) up to head_dim 192; the
 // 256-dim variant keeps 128 fp32 accumulators per lane and runs one wave per SIMD.
@@ -138,7 +65,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][S::TILE];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int g = lane >> 5;
@@ -483,7 +410,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillP
   float* of = reinterpret_cast<float*>(p.o);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int lane = tid & 63;
   const int l32 = lane & 31;
   const int g = lane >> 5;
