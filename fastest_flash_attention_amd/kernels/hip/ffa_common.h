@@ -95,6 +95,12 @@ __device__ inline float tanh_approx(float y) {
   return __builtin_copysignf(t, y);
 }
 
+// tanh(y) = 1 - 2 / (1 + e^{2y}), given x = 2y * log2(e): exp2, add, rcp, fma. It
+// saturates to -1 / +1 for large |y| (e^{2y} = 0 / inf); |error| ~ 1e-7 absolute.
+__device__ inline float tanh_fast(float x) {
+  return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + fast_exp2(x)), 1.0f);
+}
+
 // Eight consecutive 16-bit elements row[d0 .. d0+7] as one 128-bit value, zero
 // beyond `dlim`. `vec` promises 16-byte alignment of row + d0 whenever d0 + 8 <= dlim.
 __device__ inline u32x4 load_row8(const uint16_t* __restrict__ row, int d0, int dlim, bool vec) {

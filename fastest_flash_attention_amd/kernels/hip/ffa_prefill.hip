@@ -108,9 +108,11 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
       p.kmask != nullptr ? p.kmask + static_cast<int64_t>(min(qrow, p.Sq - 1) / p.ref_bq) * p.kmask_words
                          : nullptr;
 
-  // Scores stay in raw (q.k) units until the exponent: p = exp2(s*c - m*c).
-  const float c = SOFTCAP ? 1.0f : p.score_mul;
-  const float thresh = SOFTCAP ? kRescaleThresh : kRescaleThresh / p.score_mul;
+  // Scores stay in raw units until the exponent: p = exp2(s*c - m*c), with s = q.k and
+  // c = scale*log2e, or with softcap s = tanh(q.k * scale / cap) and c = cap*log2e.
+  const float c = SOFTCAP ? p.cap_mul : p.score_mul;
+  const float thresh = kRescaleThresh / c;
+  const float tanh_mul = 2.0f * kLog2e * p.score_mul;  // softcap: e^{2y} = exp2(s * tanh_mul)
 
   // ---- direct global -> LDS tile loads -------------------------------------------
   // Load j of this thread fills chunk position P = (4j + wave) * 64 + lane of the tile
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
       for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          sacc[nb][r] = p.cap_mul * tanh_approx(sacc[nb][r] * p.score_mul);
+          sacc[nb][r] = tanh_fast(sacc[nb][r] * tanh_mul);
         }
       }
     }
