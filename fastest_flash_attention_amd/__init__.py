@@ -11,6 +11,7 @@ from .modules import FastestFlashGQA, FastestFlashMHA, FastestFlashMLA
 from .ops import (
     ContinuousKVCache,
     FastestFlashAttnFunc,
+    MLALatentCache,
     PagedKVCache,
     combine_block_masks,
     create_causal_block_mask,
@@ -18,6 +19,7 @@ from .ops import (
     create_sliding_window_block_mask,
     fastest_flash_attn_forward,
     fastest_flash_attn_func,
+    fastest_flash_mla_decode,
     fastest_flash_paged_decode,
 )
 from .utils import auto_select_block_size, check_hip_available, check_triton_available
@@ -30,6 +32,8 @@ __all__ = [
     "fastest_flash_attn_func",
     "FastestFlashAttnFunc",
     "fastest_flash_paged_decode",
+    "fastest_flash_mla_decode",
+    "MLALatentCache",
     "FastestFlashMHA",
     "FastestFlashGQA",
     "FastestFlashMLA",

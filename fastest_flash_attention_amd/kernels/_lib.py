@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime before libffa.so)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libffa.so")
 
-FFA_ABI_VERSION = 2
+FFA_ABI_VERSION = 3
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
 FFA_DTYPE_FP32 = 2
@@ -136,6 +136,35 @@ class PagedDecodeArgs(ctypes.Structure):
     ]
 
 
+class MlaDecodeArgs(ctypes.Structure):
+    """Mirror of ``ffa_mla_decode_args``."""
+
+    _fields_ = [
+        ("q", ctypes.c_void_p),
+        ("kv_pages", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("block_tables", ctypes.c_void_p),
+        ("context_lens", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("q_stride", _I64x2),
+        ("o_stride", _I64x2),
+        ("lse_stride", _I64x2),
+        ("block_table_stride", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("heads_q", ctypes.c_int32),
+        ("dim_v", ctypes.c_int32),
+        ("dim_rope", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("max_context_len", ctypes.c_int32),
+        ("tokens_per_split", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 # Every symbol include/ffa.h declares, with its ctypes signature.
 EXPORTS = {
     "ffa_prefill_fwd": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]),
@@ -147,6 +176,11 @@ EXPORTS = {
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],
     ),
     "ffa_paged_decode_fwd": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), ctypes.c_void_p]),
+    "ffa_mla_decode_workspace_bytes": (
+        ctypes.c_size_t,
+        [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],
+    ),
+    "ffa_mla_decode_fwd": (ctypes.c_int, [ctypes.POINTER(MlaDecodeArgs), ctypes.c_void_p]),
     "ffa_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "ffa_abi_version": (ctypes.c_int, []),
 }

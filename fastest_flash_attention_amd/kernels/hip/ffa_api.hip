@@ -123,10 +123,11 @@ int ffa_paged_append(const ffa_paged_append_args* a, void* stream) {
     return FFA_ERR_INVALID_ARG;
   }
   if (a->n_tokens == 0) return FFA_OK;
-  if (a->k_pages == nullptr || a->v_pages == nullptr || a->k_new == nullptr ||
-      a->v_new == nullptr || a->page_table == nullptr) {
+  if (a->k_pages == nullptr || a->k_new == nullptr || a->page_table == nullptr) {
     return FFA_ERR_INVALID_ARG;
   }
+  // V is optional (K-only pools), but then entirely
+  if ((a->v_pages == nullptr) != (a->v_new == nullptr)) return FFA_ERR_INVALID_ARG;
   for (int i = 0; i < 2; ++i) {
     if (a->k_new_stride[i] < 0 || a->v_new_stride[i] < 0) return FFA_ERR_INVALID_ARG;
   }
@@ -182,6 +183,50 @@ int ffa_paged_decode_fwd(const ffa_paged_decode_args* a, void* stream) {
   if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need)) return FFA_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 15u) != 0) return FFA_ERR_MISALIGNED;
   return ffa::launch_paged_decode(*a, static_cast<hipStream_t>(stream));
+}
+
+size_t ffa_mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,
+                                      int32_t max_context_len, int32_t tokens_per_split) {
+  if (batch < 0 || heads_q < 0 || dim_v < 0 || max_context_len < 0) return 0;
+  return ffa::mla_decode_workspace_bytes(batch, heads_q, dim_v, max_context_len,
+                                         tokens_per_split);
+}
+
+int ffa_mla_decode_fwd(const ffa_mla_decode_args* a, void* stream) {
+  if (a == nullptr) return FFA_ERR_INVALID_ARG;
+  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if ((a->dim_v != 256 && a->dim_v != 512) || a->dim_rope != 64) {
+    return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  }
+  if (a->batch < 0 || a->heads_q < 1 || a->page_size < 1 || a->num_pages < 0 ||
+      a->max_context_len < 0 || a->tokens_per_split < 0) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->batch == 0) return FFA_OK;
+  if (a->q == nullptr || a->o == nullptr || a->kv_pages == nullptr ||
+      a->block_tables == nullptr || a->context_lens == nullptr) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  const int64_t max_blocks =
+      (static_cast<int64_t>(a->max_context_len) + a->page_size - 1) / a->page_size;
+  if (a->block_table_stride < max_blocks) return FFA_ERR_INVALID_ARG;
+  for (int i = 0; i < 2; ++i) {
+    if (a->q_stride[i] < 0 || a->o_stride[i] < 0 || a->lse_stride[i] < 0) {
+      return FFA_ERR_INVALID_ARG;
+    }
+  }
+  if (!(a->scale == a->scale)) return FFA_ERR_INVALID_ARG;
+  if (a->max_context_len > 0 && a->num_pages < 1) return FFA_ERR_INVALID_ARG;
+  if ((reinterpret_cast<uintptr_t>(a->q) & 15u) != 0 ||
+      (reinterpret_cast<uintptr_t>(a->kv_pages) & 15u) != 0) {
+    return FFA_ERR_MISALIGNED;
+  }
+  if (a->q_stride[0] % 8 != 0 || a->q_stride[1] % 8 != 0) return FFA_ERR_MISALIGNED;
+  const size_t need = ffa::mla_decode_workspace_bytes(a->batch, a->heads_q, a->dim_v,
+                                                      a->max_context_len, a->tokens_per_split);
+  if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need)) return FFA_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 15u) != 0) return FFA_ERR_MISALIGNED;
+  return ffa::launch_mla_decode(*a, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

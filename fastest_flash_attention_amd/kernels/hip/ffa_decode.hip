@@ -427,6 +427,261 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p
   }
 }
 
+// ---------------------------------------------------------------------------------
+// MLA decode over the compressed latent cache (absorbed form of the reference
+// FastestFlashMLA attention, modules/flash_mla.py:116-172). With W_uk / W_uv the
+// per-head slices of kv_up_proj, head h scores token t as
+//   q_nope.(W_uk c_t) + q_rope.r_t = [W_uk^T q_nope, q_rope] . [c_t, r_t]
+// and outputs sum_t p_t W_uv c_t = W_uv (sum_t p_t c_t). So every head attends over
+// ONE shared KV row per token, [c_t (DV dims) | r_t (64 rope dims)], with V = its first
+// DV dims: an MQA decode with D_qk = DV + 64, D_v = DV, whose latent-space output the
+// host up-projects with W_uv. Each token costs (DV + 64) * 2 bytes for all heads.
+//
+// Pool layout: [num_pages, page_size, DV + 64], token t of sequence b at page
+// block_tables[b][t / page_size], slot t % page_size (the PagedKVCache index law).
+// Workgroup = 8 waves for (split, 32-head group, sequence). 32-key tiles of the shared
+// rows go HBM -> LDS (waves 0-3 issue, asm global_load_lds_dwordx4) into a 3-stage ring
+// with one barrier per tile. Wave w takes heads 16 * (w >> 2) + 0..15 (MFMA columns)
+// and output dims [(w & 3) DV/4, (w & 3 + 1) DV/4): it computes S^T = K Q^T for its 16
+// heads with v_mfma_f32_16x16x32 (the 4 waves of a head group duplicate this small
+// product rather than exchanging P), fp32 softmax with exp2 and deferred rescale, and
+// O^T += V^T P^T with v_mfma_f32_16x16x16 on its DV/4 dims (V^T by ds_read_b64_tr_b16).
+// Normalised (O, lse) partials per split are merged by decode_combine_kernel.
+// ---------------------------------------------------------------------------------
+constexpr int kMlaWaves = 8;
+constexpr int kMlaThreads = 64 * kMlaWaves;
+constexpr int kMlaTile = 32;
+constexpr int kMlaStages = 3;
+constexpr int kMlaRope = 64;
+constexpr int kMlaMaxSplit = 1024;
+constexpr int kMlaDefaultSplit = 512;
+
+struct MlaParams {
+  const uint16_t* q;
+  const uint16_t* kv;
+  const int32_t* bt;
+  const int32_t* lens;
+  float* ws_o;
+  float* ws_lse;
+  int64_t q_sb, q_sh;
+  int bt_stride;
+  int B, Hq, P, log2P, num_pages;
+  int n_splits, tps, max_len;
+  float score_mul;  // scale * log2e
+};
+
+__device__ inline int mla_page_of(const MlaParams& p, int tok, int& slot) {
+  if (p.log2P >= 0) {
+    slot = tok & (p.P - 1);
+    return tok >> p.log2P;
+  }
+  const int pi = tok / p.P;
+  slot = tok - pi * p.P;
+  return pi;
+}
+
+// XOR swizzle of 16-byte chunks inside each aligned group of 8: a row is (DV+64)*2 bytes
+// = 8 (mod 16) chunks, so rows r and r+2 would share banks; (r >> 1) & 7 spreads the 16
+// rows of a K operand read, and the 4 rows of a transposed V read, over distinct banks.
+__device__ inline int mla_swz(int r) { return (r >> 1) & 7; }
+
+template <typename Tag, int DV>
+__global__ __launch_bounds__(kMlaThreads, 1) void mla_decode_split_kernel(const MlaParams p) {
+  using E = Elem<Tag>;
+  constexpr int DQK = DV + kMlaRope;
+  constexpr int CH = DQK / 8;                  // 16-byte chunks per row
+  constexpr int TILE = kMlaTile * DQK;         // elements per tile
+  constexpr int LPT = kMlaTile * CH / 256;     // loads per issuing lane per tile
+  constexpr int KS = DQK / 32;                 // QK k-steps
+  constexpr int DW = DV / 4;                   // output dims per wave
+  constexpr int DBW = DW / 16;                 // 16-dim output blocks per wave
+  static_assert(CH % 8 == 0 && kMlaTile * CH % 256 == 0, "row / tile shape");
+  __shared__ __attribute__((aligned(1024))) uint16_t ring[kMlaStages][TILE];
+  __shared__ int bt_lds[kMlaMaxSplit + 2];
+
+  const int split = blockIdx.x;
+  const int hg = blockIdx.y;
+  const int b = blockIdx.z;
+  const int L = min(max(p.lens[b], 0), p.max_len);
+  const int s_begin = split * p.tps;
+  const int s_end = min(s_begin + p.tps, L);
+  if (s_begin >= s_end) return;  // uniform across the workgroup: no barrier reached
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int hs = wave >> 2;  // head subgroup: MFMA columns = heads 16 hs + c16
+  const int dq = wave & 3;   // output dim quarter
+  const int head = hg * 32 + hs * 16 + c16;
+  const bool head_live = head < p.Hq;
+  const bool issuer = wave < 4;
+
+  int slot0;
+  const int pg0 = mla_page_of(p, s_begin, slot0);
+  int slot1;
+  const int pg1 = mla_page_of(p, s_end - 1, slot1);
+  {
+    const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+    for (int i = tid; i <= pg1 - pg0; i += kMlaThreads) {
+      const int phys = btrow[pg0 + i];
+      bt_lds[i] = (phys >= 0 && phys < p.num_pages) ? phys : 0;
+    }
+  }
+  // Q^T as the B operand: lane holds head `head`, dims 32 ks + 8 g4 .. +7.
+  u32x4 qreg[KS];
+  {
+    const uint16_t* qr = p.q + b * p.q_sb + static_cast<int64_t>(head_live ? head : 0) * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * g4);
+      qreg[ks] = head_live ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // Compiler-issued loads (block table, Q) complete before the asm tile loads start.
+  wait_vmcnt0();
+  __syncthreads();
+
+  const char* pool = reinterpret_cast<const char*>(p.kv);
+  const int n_tiles = (s_end - s_begin + kMlaTile - 1) / kMlaTile;
+  // Issuing lanes: load j fills chunk position P = (4j + wave) * 64 + lane of a tile.
+  auto issue = [&](int t, int st) {
+    const int t0 = s_begin + t * kMlaTile;
+    uint16_t* dst = ring[st];
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / CH;
+      const int pc = pos - row * CH;
+      const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
+      int slot;
+      const int pg = mla_page_of(p, tok, slot);
+      const int64_t ro = (static_cast<int64_t>(bt_lds[pg - pg0]) * p.P + slot) * DQK * 2;
+      load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (4 * j + wave) * 512));
+    }
+  };
+
+  // Per-lane operand offsets (elements) inside a tile. K operand of k-step ks, key block
+  // kb: row 16 kb + c16, chunk 4 ks + g4; the swizzle depends on c16 only, so k-steps
+  // two apart differ by 64 elements and key blocks by 16 rows.
+  const int ksw = mla_swz(c16);
+  const int k_rd0 = c16 * DQK + (((0 + g4) ^ ksw) << 3);
+  const int k_rd1 = c16 * DQK + (((4 + g4) ^ ksw) << 3);
+  // V^T operand of dim block db (ds_read_b64_tr_b16 law): this lane supplies key row
+  // 16 kb + 4 g4 + (c16 >> 2) and dims 4 (c16 & 3) .. +3 of the 16-dim block.
+  const int vrow = 4 * g4 + (c16 >> 2);
+  const int vsw = mla_swz(vrow);
+  int v_rd[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int col = dq * DW + 16 * u + 4 * (c16 & 3);
+    v_rd[u] = vrow * DQK + (((col >> 3) ^ vsw) << 3) + (col & 7);
+  }
+
+  f32x4 oacc[DBW];
+#pragma unroll
+  for (int db = 0; db < DBW; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf;
+  float l_run = 0.0f;
+
+  auto compute = [&](int t, const uint16_t* tl) {
+    const int t0 = s_begin + t * kMlaTile;
+    f32x4 sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = ((ks & 1) ? k_rd1 : k_rd0) + (ks >> 1) * 64 + kb * 16 * DQK;
+        const u32x4 a = *reinterpret_cast<const u32x4*>(tl + off);
+        sacc[kb] = E::mfma16(a, qreg[ks], sacc[kb]);
+      }
+    }
+    // S^T lane layout: keys 16 kb + 4 g4 + j of head c16
+    float mt = kNegInf;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = t0 + 16 * kb + 4 * g4 + j;
+        const float x = tok < s_end ? sacc[kb][j] * p.score_mul : kNegInf;
+        sacc[kb][j] = x;
+        mt = fmaxf(mt, x);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = wave_pair_max(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const bool need = m_new > m_run + kRescaleThresh;
+    if (__any(need)) {
+      const float alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
+      m_run = need ? m_new : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DBW; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) oacc[db][j] *= alpha;
+      }
+    }
+    const float mu = (m_run == kNegInf) ? 0.0f : m_run;
+    u32x2 pk[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float e[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e[j] = fast_exp2(sacc[kb][j] - mu);
+        l_run += e[j];
+      }
+      pk[kb] = u32x2{E::pack2(e[0], e[1]), E::pack2(e[2], e[3])};
+    }
+#pragma unroll
+    for (int db = 0; db < DBW; ++db) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int off = v_rd[db & 3] + (db >> 2) * 64 + kb * 16 * DQK;
+        const u32x2 a = lds_read_tr16(tl + off);  // dim 16 db + c16 of keys 4 g4 + 0..3
+        oacc[db] = E::mfma16k16(a, pk[kb], oacc[db]);
+      }
+    }
+  };
+
+  if (issuer) {
+    issue(0, 0);
+    if (n_tiles > 1) issue(1, 1);
+  }
+  for (int t = 0; t < n_tiles; ++t) {
+    if (issuer) {
+      if (t + 1 < n_tiles) {
+        wait_vmcnt<LPT>();
+      } else {
+        wait_vmcnt0();
+      }
+    }
+    __syncthreads();  // tile t is in LDS; every wave is done with tile t-1
+    if (issuer && t + 2 < n_tiles) issue(t + 2, (t + 2) % kMlaStages);
+    compute(t, ring[t % kMlaStages]);
+  }
+
+  // Partial of this split: O^T lane layout dims 16 db + 4 g4 + j (of this wave's
+  // quarter) for head c16.
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot = wave_pair_sum(l_tot);
+  if (!head_live) return;
+  const int64_t row = (static_cast<int64_t>(b) * p.Hq + head) * p.n_splits + split;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  float* wo = p.ws_o + row * DV + dq * DW + 4 * g4;
+#pragma unroll
+  for (int db = 0; db < DBW; ++db) {
+    const f32x4 v = {oacc[db][0] * inv, oacc[db][1] * inv, oacc[db][2] * inv, oacc[db][3] * inv};
+    *reinterpret_cast<f32x4*>(wo + 16 * db) = v;
+  }
+  if (dq == 0 && g4 == 0) {
+    p.ws_lse[row] = l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : kNegInf;
+  }
+}
+
 // get_kv: copy the first context_len tokens of one sequence into [H, L, D].
 template <typename U>
 __global__ __launch_bounds__(256) void paged_gather_kernel(const U* __restrict__ kp,
@@ -478,7 +733,7 @@ __global__ __launch_bounds__(256) void paged_append_kernel(
     const int slot = pos - (pos / P) * P;
     const int64_t dst = ((static_cast<int64_t>(phys) * H + h) * P + slot) * row_units + u;
     kp[dst] = kn[h * k_sh + t * k_st + u];
-    vp[dst] = vn[h * v_sh + t * v_st + u];
+    if (vp != nullptr) vp[dst] = vn[h * v_sh + t * v_st + u];
   }
 }
 
@@ -667,6 +922,95 @@ int launch_paged_append(const ffa_paged_append_args& a, hipStream_t stream) {
     run(uint16_t{}, 2);
   } else {
     return FFA_ERR_MISALIGNED;  // 4-byte elements off 4-byte alignment
+  }
+  return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
+}
+
+
+int32_t mla_decode_tokens_per_split(int32_t tokens_per_split) {
+  if (tokens_per_split <= 0) return kMlaDefaultSplit;
+  const int32_t t = ((tokens_per_split + kMlaTile - 1) / kMlaTile) * kMlaTile;
+  return t > kMlaMaxSplit ? kMlaMaxSplit : t;
+}
+
+int32_t mla_decode_num_splits(int32_t max_context_len, int32_t tokens_per_split) {
+  const int32_t tps = mla_decode_tokens_per_split(tokens_per_split);
+  return max_context_len <= 0 ? 1 : (max_context_len + tps - 1) / tps;
+}
+
+size_t mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,
+                                  int32_t max_context_len, int32_t tokens_per_split) {
+  const size_t ns = static_cast<size_t>(mla_decode_num_splits(max_context_len, tokens_per_split));
+  const size_t rows = static_cast<size_t>(batch) * heads_q * ns;
+  return rows * (static_cast<size_t>(dim_v) + 1) * sizeof(float);
+}
+
+namespace {
+
+template <typename Tag>
+void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3 grid,
+                    hipStream_t s) {
+  if (dim_v == 512) {
+    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512>), grid, dim3(kMlaThreads), 0, s, mp);
+  } else {
+    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256>), grid, dim3(kMlaThreads), 0, s, mp);
+  }
+  hipLaunchKernelGGL((decode_combine_kernel<Tag>), dim3(cp.B * cp.Hq), dim3(64), 0, s, cp);
+}
+
+}  // namespace
+
+int launch_mla_decode(const ffa_mla_decode_args& a, hipStream_t stream) {
+  MlaParams mp{};
+  mp.q = static_cast<const uint16_t*>(a.q);
+  mp.kv = static_cast<const uint16_t*>(a.kv_pages);
+  mp.bt = a.block_tables;
+  mp.lens = a.context_lens;
+  mp.q_sb = a.q_stride[0];
+  mp.q_sh = a.q_stride[1];
+  mp.bt_stride = a.block_table_stride;
+  mp.B = a.batch;
+  mp.Hq = a.heads_q;
+  mp.P = a.page_size;
+  mp.log2P = ((a.page_size & (a.page_size - 1)) == 0) ? __builtin_ctz(a.page_size) : -1;
+  mp.num_pages = a.num_pages;
+  mp.tps = mla_decode_tokens_per_split(a.tokens_per_split);
+  mp.n_splits = mla_decode_num_splits(a.max_context_len, a.tokens_per_split);
+  mp.max_len = a.max_context_len;
+  mp.score_mul = a.scale * kLog2e;
+  const size_t rows = static_cast<size_t>(a.batch) * a.heads_q * mp.n_splits;
+  mp.ws_o = static_cast<float*>(a.workspace);
+  mp.ws_lse = mp.ws_o + rows * a.dim_v;
+
+  // the split-K merge is the paged-decode combine kernel over dim_v output dims
+  DecodeParams cp{};
+  cp.o = static_cast<uint16_t*>(a.o);
+  cp.lse = a.lse;
+  cp.lens = a.context_lens;
+  cp.ws_o = mp.ws_o;
+  cp.ws_lse = mp.ws_lse;
+  cp.o_sb = a.o_stride[0];
+  cp.o_sh = a.o_stride[1];
+  cp.l_sb = a.lse_stride[0];
+  cp.l_sh = a.lse_stride[1];
+  cp.B = a.batch;
+  cp.Hq = a.heads_q;
+  cp.D = a.dim_v;
+  cp.dp = a.dim_v;
+  cp.n_splits = mp.n_splits;
+  cp.tps = mp.tps;
+  cp.window = 0;
+  cp.max_len = a.max_context_len;
+
+  const int64_t gy = (static_cast<int64_t>(a.heads_q) + 31) / 32;
+  if (gy > 65535 || a.batch > 65535 || static_cast<int64_t>(a.batch) * a.heads_q > 0x7fffffff) {
+    return FFA_ERR_TOO_LARGE;
+  }
+  const dim3 grid(mp.n_splits, static_cast<unsigned>(gy), a.batch);
+  if (a.dtype == FFA_DTYPE_BF16) {
+    launch_mla_tag<Bf16Tag>(mp, cp, a.dim_v, grid, stream);
+  } else {
+    launch_mla_tag<F16Tag>(mp, cp, a.dim_v, grid, stream);
   }
   return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
 }

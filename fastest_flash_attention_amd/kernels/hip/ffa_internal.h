@@ -18,6 +18,13 @@ size_t decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
                               int32_t max_context_len, int32_t tokens_per_split);
 int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream);
 
+// MLA decode over the compressed latent cache: split kernel + the decode combine kernel.
+int32_t mla_decode_tokens_per_split(int32_t tokens_per_split);
+int32_t mla_decode_num_splits(int32_t max_context_len, int32_t tokens_per_split);
+size_t mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,
+                                  int32_t max_context_len, int32_t tokens_per_split);
+int launch_mla_decode(const ffa_mla_decode_args& a, hipStream_t stream);
+
 // get_kv gather.
 int launch_paged_gather(const ffa_paged_gather_args& a, hipStream_t stream);
 int launch_paged_append(const ffa_paged_append_args& a, hipStream_t stream);

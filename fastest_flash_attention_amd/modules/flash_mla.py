@@ -9,13 +9,14 @@ num_heads * D. The attention core is the HIP forward.
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Optional, Sequence
 
 import torch
 import torch.nn as nn
 
 from ..ops.attention_forward import fastest_flash_attn_forward
 from ..ops.attention_func import fastest_flash_attn_func
+from ..ops.mla_decode import MLALatentCache
 
 
 class RotaryEmbedding(nn.Module):
@@ -38,6 +39,21 @@ class RotaryEmbedding(nn.Module):
         half = x.size(-1) // 2
         cos = emb.cos()[None, None, :, :half]
         sin = emb.sin()[None, None, :, :half]
+        x1 = x[..., :half]
+        x2 = x[..., half:]
+        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
+
+    def rotate_at(self, x: torch.Tensor, positions: Sequence[int]) -> torch.Tensor:
+        """RoPE of one token per batch row: x ``[B, ..., D_rope]``, token of row b at
+        ``positions[b]``. Bitwise the rotation ``forward`` applies at that position
+        (positions in the input dtype, fp32 angles)."""
+        pos = torch.tensor(list(positions), dtype=x.dtype, device=x.device)
+        freqs = pos.float()[:, None] * self.inv_freq.to(x.device)[None, :]
+        emb = torch.cat([freqs, freqs], dim=-1)
+        half = x.size(-1) // 2
+        shape = (x.size(0),) + (1,) * (x.dim() - 2) + (half,)
+        cos = emb.cos()[:, :half].reshape(shape)
+        sin = emb.sin()[:, :half].reshape(shape)
         x1 = x[..., :half]
         x2 = x[..., half:]
         return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(x.dtype)
@@ -103,6 +119,68 @@ class FastestFlashMLA(nn.Module):
             attn, _ = fastest_flash_attn_forward(q, k, v_padded, scale=self.scale,
                                                  causal=use_causal, block_size=bs)
         return self.o_proj(attn.transpose(1, 2).contiguous().view(B, S, -1))
+
+    # ---- decode over the compressed latent cache (no counterpart in the reference) ----
+
+    def absorbed_weights(self):
+        """Per-head ``(W_uk, W_uv)``, each ``[H, head_dim, latent_dim]``: the K_nope and V
+        rows of kv_up_proj (reference :102-104, :141-144 split its output per head as
+        [K_nope | V])."""
+        w = self.kv_up_proj.weight.view(self.num_heads, 2 * self.head_dim, self.latent_dim)
+        return w[:, : self.head_dim], w[:, self.head_dim:]
+
+    def new_latent_cache(self, max_pages: int, page_size: int = 64) -> MLALatentCache:
+        w = self.kv_up_proj.weight
+        return MLALatentCache(max_pages=max_pages, page_size=page_size,
+                              latent_dim=self.latent_dim, rope_dim=self.rope_dim,
+                              dtype=w.dtype, device=w.device)
+
+    def prefill_with_cache(self, x: torch.Tensor, cache: MLALatentCache,
+                           seq_ids: Sequence[int]) -> torch.Tensor:
+        """``forward(x)`` (causal prompt of new sequences ``seq_ids``, positions 0..S-1)
+        that also stores every token's latent row ``[c_t | r_t]`` in ``cache``."""
+        if any(cache.seq_len(s) != 0 for s in seq_ids):
+            raise ValueError("prefill_with_cache starts new sequences (positions 0..S-1)")
+        B, S, _ = x.shape
+        out = self.forward(x, causal=True)
+        latent = self.kv_down_proj(x)                               # [B, S, latent]
+        k_rope = self.rope(self.k_rope_proj(x).unsqueeze(1))[:, 0]  # [B, S, rope]
+        for i, sid in enumerate(seq_ids):
+            cache.append(sid, latent[i], k_rope[i])
+        return out
+
+    def decode_step(self, x: torch.Tensor, cache: MLALatentCache, seq_ids: Sequence[int],
+                    return_attention: bool = False):
+        """One new token per sequence: x ``[B, 1, hidden]`` -> ``[B, 1, hidden]``.
+
+        The token's latent row is appended at position ``len(seq)``, then every head
+        attends over the sequence's cached rows through ``ffa_mla_decode_fwd`` with the
+        absorbed query ``[W_uk^T q_nope, q_rope]``; the latent output is up-projected by
+        W_uv and zero-padded over the rope dims as the reference pads V (:152). The
+        result is the reference forward of the whole sequence at its last position.
+        With ``return_attention`` also the attention output ``[B, H, head_dim + rope]``.
+        """
+        B = x.size(0)
+        H, hd, R, lat = self.num_heads, self.head_dim, self.rope_dim, self.latent_dim
+        if x.dim() != 3 or x.size(1) != 1 or len(seq_ids) != B:
+            raise ValueError("decode_step takes x [B, 1, hidden] and one seq id per row")
+        pos = [cache.seq_len(s) for s in seq_ids]
+        q_nope = self.q_proj(x).view(B, H, hd)
+        q_rope = self.rope.rotate_at(self.q_rope_proj(x).view(B, H, R), pos)
+        latent = self.kv_down_proj(x).view(B, lat)
+        k_rope = self.rope.rotate_at(self.k_rope_proj(x).view(B, R), pos)
+        for i, sid in enumerate(seq_ids):
+            cache.append(sid, latent[i:i + 1], k_rope[i:i + 1])
+        w_uk, w_uv = self.absorbed_weights()
+        # batched products over heads, operands contiguous (no transposed views)
+        q_lat = torch.bmm(q_nope.transpose(0, 1).contiguous(), w_uk.contiguous())  # [H, B, lat]
+        q_abs = torch.cat([q_lat.transpose(0, 1), q_rope], dim=-1).contiguous()
+        o_lat, _ = cache.decode(q_abs, seq_ids, scale=self.scale)                 # [B, H, lat]
+        o = torch.bmm(o_lat.transpose(0, 1).contiguous(),
+                      w_uv.transpose(1, 2).contiguous()).transpose(0, 1)          # [B, H, hd]
+        attn = torch.cat([o, o.new_zeros(B, H, R)], dim=-1)
+        out = self.o_proj(attn.reshape(B, 1, H * (hd + R)))
+        return (out, attn) if return_attention else out
 
     def extra_repr(self) -> str:
         return (

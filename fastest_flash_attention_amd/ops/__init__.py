@@ -10,6 +10,7 @@ from .block_sparse import (
     create_sliding_window_block_mask,
 )
 from .kv_cache import ContinuousKVCache, PagedKVCache, fastest_flash_paged_decode
+from .mla_decode import MLALatentCache, fastest_flash_mla_decode
 
 __all__ = [
     "fastest_flash_attn_forward",
@@ -18,6 +19,8 @@ __all__ = [
     "ContinuousKVCache",
     "PagedKVCache",
     "fastest_flash_paged_decode",
+    "MLALatentCache",
+    "fastest_flash_mla_decode",
     "create_causal_block_mask",
     "create_sliding_window_block_mask",
     "create_local_block_mask",

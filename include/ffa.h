@@ -22,6 +22,12 @@
  *   ffa_paged_decode_workspace_bytes, ffa_paged_decode_num_splits: sizing helpers of
  *                             the decode entry point (no reference counterpart; the
  *                             reference has no fused decode).
+ *   ffa_mla_decode_fwd     <- FastestFlashMLA attention for one new token
+ *                             (modules/flash_mla.py:116-172, reached with the up-projected
+ *                              K/V of all previous tokens as kv_cache): the reference has
+ *                              no MLA decode path; this one reads the compressed latent
+ *                              cache instead of up-projected K/V.
+ *   ffa_mla_decode_workspace_bytes: sizing helper of the MLA decode entry point.
  *   ffa_strerror, ffa_abi_version: error text / version probe, replacing the
  *                             availability probe check_triton_available utils.py:20-29.
  */
@@ -35,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FFA_ABI_VERSION 2
+#define FFA_ABI_VERSION 3
 
 typedef enum ffa_status {
   FFA_OK = 0,
@@ -152,7 +158,8 @@ int ffa_paged_gather(const ffa_paged_gather_args* args, void* stream);
  * (page_table holds >= ceil((start + n_tokens) / page_size) valid ids, each in
  * [0, num_pages); FFA_ERR_INVALID_ARG is not detected on the device for bad ids,
  * which are skipped). k_new / v_new are [heads_kv, n_tokens, head_dim] with element
- * strides new_stride[head, token] (dim stride 1) and the pool's dtype.
+ * strides new_stride[head, token] (dim stride 1) and the pool's dtype. v_pages and v_new
+ * may both be NULL: a K-only append (the MLA latent pool, one row per token).
  */
 typedef struct ffa_paged_append_args {
   void* k_pages;
@@ -226,6 +233,53 @@ int32_t ffa_paged_decode_num_splits(int32_t max_context_len, int32_t tokens_per_
 size_t ffa_paged_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
                                         int32_t max_context_len, int32_t tokens_per_split);
 int ffa_paged_decode_fwd(const ffa_paged_decode_args* args, void* stream);
+
+/*
+ * MLA decode over the compressed latent cache (no counterpart in the reference, which
+ * up-projects K/V per head; see FastestFlashMLA, modules/flash_mla.py:116-172). Every
+ * query head attends over one shared row per token,
+ *   kv_pages : [num_pages, page_size, dim_v + dim_rope], contiguous: the latent c_t
+ *              (dim_v) followed by the rotated k_rope r_t (dim_rope),
+ * with the absorbed query q_h = [W_uk_h^T q_nope_h, q_rope_h] and V = the first dim_v
+ * dims of the row. Scores are scale * q_h . row_t over the first context_lens[b] tokens
+ * (page index law as for the paged pools); the output is the latent-space
+ * O_lat_h = sum_t p_t c_t, which the caller up-projects with W_uv_h.
+ *   q   : [batch, heads_q, dim_v + dim_rope] (strides q_stride[b, h], dim stride 1)
+ *   o   : [batch, heads_q, dim_v] (strides o_stride[b, h])
+ *   lse : [batch, heads_q] fp32 (strides lse_stride[b, h]) or NULL
+ * dim_v is 256 or 512 and dim_rope is 64 (FFA_ERR_UNSUPPORTED_HEAD_DIM). q and
+ * kv_pages are 16-byte aligned, q's strides multiples of 8 (FFA_ERR_MISALIGNED).
+ * tokens_per_split (0: library default 512) is rounded up to a multiple of 32 and
+ * capped at 1024; partials go to the workspace as in ffa_paged_decode_fwd.
+ */
+typedef struct ffa_mla_decode_args {
+  const void* q;
+  const void* kv_pages;
+  void* o;
+  float* lse;
+  const int32_t* block_tables;   /* [batch, block_table_stride] int32 */
+  const int32_t* context_lens;   /* [batch] int32 */
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t q_stride[2];
+  int64_t o_stride[2];
+  int64_t lse_stride[2];
+  int32_t block_table_stride;
+  int32_t batch;
+  int32_t heads_q;
+  int32_t dim_v;                 /* 256 or 512 */
+  int32_t dim_rope;              /* 64 */
+  int32_t page_size;
+  int32_t num_pages;
+  int32_t max_context_len;
+  int32_t tokens_per_split;      /* 0: library default */
+  float scale;
+  int32_t dtype;                 /* FFA_DTYPE_BF16 or FFA_DTYPE_FP16 */
+} ffa_mla_decode_args;
+
+size_t ffa_mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,
+                                      int32_t max_context_len, int32_t tokens_per_split);
+int ffa_mla_decode_fwd(const ffa_mla_decode_args* args, void* stream);
 
 const char* ffa_strerror(int status);
 int ffa_abi_version(void);

@@ -150,6 +150,7 @@ def _c_layout(struct: str, fields: list[str]) -> dict:
     (_lib.PagedGatherArgs, "ffa_paged_gather_args"),
     (_lib.PagedDecodeArgs, "ffa_paged_decode_args"),
     (_lib.PagedAppendArgs, "ffa_paged_append_args"),
+    (_lib.MlaDecodeArgs, "ffa_mla_decode_args"),
 ])
 def test_ctypes_struct_matches_header(cls, cname):
     fields = [f for f, _ in cls._fields_]
@@ -190,6 +191,27 @@ def test_validation_errors_without_device(lib):
     g = _lib.PagedGatherArgs()
     g.elem_bytes = 3
     assert lib.ffa_paged_gather(ctypes.byref(g), None) == -2
+    ap = _lib.PagedAppendArgs()
+    ap.elem_bytes, ap.heads_kv, ap.page_size, ap.head_dim, ap.n_tokens, ap.num_pages = 2, 1, 16, 576, 3, 4
+    ap.k_pages = ap.k_new = ap.page_table = 16
+    ap.v_new = 16  # V given without its pool: K-only appends pass neither
+    assert lib.ffa_paged_append(ctypes.byref(ap), None) == -1
+    m = _lib.MlaDecodeArgs()
+    assert lib.ffa_mla_decode_fwd(None, None) == -1
+    m.dtype, m.dim_v, m.dim_rope, m.batch, m.heads_q, m.page_size = 0, 512, 32, 2, 32, 16
+    assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -3  # rope dims must be 64
+    m.dim_rope, m.dim_v = 64, 128
+    assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -3  # latent 256 or 512
+    m.dim_v, m.dtype = 512, 2
+    assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -2  # no fp32 MLA kernel
+    m.dtype, m.max_context_len, m.block_table_stride, m.num_pages = 0, 64, 4, 8
+    m.q = m.o = m.kv_pages = m.block_tables = m.context_lens = 16
+    m.workspace, m.workspace_bytes = 16, 8
+    assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -6
+    m.q = 24
+    assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -4  # q not 16-byte aligned
+    m.q, m.block_table_stride = 16, 3
+    assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -1
 
 
 def test_workspace_sizing(lib):
@@ -200,6 +222,11 @@ def test_workspace_sizing(lib):
     assert lib.ffa_paged_decode_num_splits(100, 40) == 3  # 40 rounds up to 48 (16-token tiles)
     assert lib.ffa_paged_decode_workspace_bytes(64, 32, 128, 32768, 512) == 64 * 32 * 64 * 129 * 4
     assert lib.ffa_paged_decode_workspace_bytes(2, 4, 100, 100, 64) == 2 * 4 * 2 * 129 * 4
+    # MLA: 32-token tiles, default split 512, capped at 1024; dim_v-wide partials
+    assert lib.ffa_mla_decode_workspace_bytes(32, 32, 512, 4096, 512) == 32 * 32 * 8 * 513 * 4
+    assert lib.ffa_mla_decode_workspace_bytes(2, 8, 256, 1000, 0) == 2 * 8 * 2 * 257 * 4
+    assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 5000, 4096) == 5 * 513 * 4
+    assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 100, 40) == 2 * 513 * 4  # 40 -> 64
 
 
 # ---------------------------------------------------------------------------------
