@@ -5,7 +5,8 @@ Headline workload: bf16 causal prefill, B=4, H=32, S=
 D=128, through the drop-in ``fastest_flash_attn_forward``. A step is one forward over
 that batch with q/k/v already resident in HBM. Second workload in the same line:
 paged GQA decode (BASELINE cfg4: B=64, 32 q heads / 8 kv heads, D=128, page 16,
-context lengths U[512, 32768], random page permutation).
+context lengths U[512, 32768], random page permutation), and a third: MLA decode over
+the compressed latent cache (BASELINE cfg5 decode: batch 32 at context 4096).
 
 Algorithmic work: prefill FLOPs = 4 * B * H * D * N_valid, N_valid = exact number of
 unmasked (q, k) pairs; decode bytes = K/V bytes of exactly context_len tokens + q + o +
@@ -236,6 +237,46 @@ def bench_decode(steps: int, warmup: int):
     }
 
 
+def bench_mla_decode(steps: int, warmup: int):
+    """cfg5 decode: MLA layer (32 heads, latent 512, rope 64), batch 32 at context 4096,
+    over the compressed latent cache (ffa_mla_decode_fwd). Bytes = the latent rows of
+    exactly context_len tokens + absorbed q + latent o + lse + block tables."""
+    import torch
+
+    import fastest_flash_attention_amd as ffa
+
+    B, H, L, lat, R, P = 32, 32, 4096, 512, 64, 64
+    gd = torch.Generator(device="cuda").manual_seed(0)
+    n_pages = B * L // P
+    pool = torch.randn(n_pages, P, lat + R, generator=gd, device="cuda").to(torch.bfloat16)
+    perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(0)).to(torch.int32)
+    bt = perm.view(B, L // P).contiguous().cuda()
+    lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
+    q = torch.randn(B, H, lat + R, generator=gd, device="cuda").to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(128 + R)  # the module's 1/sqrt(head_dim + rope_dim)
+
+    def step():
+        ffa.fastest_flash_mla_decode(q, pool, bt, lens, dim_v=lat, scale=scale, return_lse=True,
+                                     max_context_len=L)
+
+    ms_event, ms_wall = time_steps(step, steps, warmup)
+    nbytes = B * L * (lat + R) * 2 + B * H * (lat + R) * 2 + B * H * lat * 2 + B * H * 4 + \
+        n_pages * 4
+    achieved = nbytes / (ms_event * 1e-3) / 1e9
+    return {
+        "metric": "MLA latent-cache decode HBM GB/s",
+        "value": nbytes / (ms_wall * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "ms_per_step": ms_wall,
+        "kernel_ms": ms_event,
+        "bytes": nbytes,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None},
+        "config": {"workload": "cfg5_mla_decode", "batch": B, "heads_q": H, "latent_dim": lat,
+                   "rope_dim": R, "context_len": L, "page_size": P},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -272,6 +313,7 @@ def main() -> int:
         del src, dst
     pre = bench_prefill(args.workload, args.steps, args.warmup, args.cpu_seconds)
     dec = None if args.no_decode else bench_decode(args.steps, args.warmup)
+    mla = None if args.no_decode else bench_mla_decode(args.steps, args.warmup)
     line = {
         "metric": "prefill attn TFLOP/s (% bf16 MFMA peak); paged-decode HBM GB/s (% peak)",
         "value": pre["value"],
@@ -289,6 +331,7 @@ def main() -> int:
         "roofline": pre["roofline"],
         "cpu_baseline": pre["cpu_baseline"],
         "decode": dec,
+        "mla_decode": mla,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -439,19 +439,19 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p
 //
 // Pool layout: [num_pages, page_size, DV + 64], token t of sequence b at page
 // block_tables[b][t / page_size], slot t % page_size (the PagedKVCache index law).
-// Workgroup = 8 waves for (split, 32-head group, sequence). 32-key tiles of the shared
-// rows go HBM -> LDS (waves 0-3 issue, asm global_load_lds_dwordx4) into a 3-stage ring
-// with one barrier per tile. Wave w takes heads 16 * (w >> 2) + 0..15 (MFMA columns)
-// and output dims [(w & 3) DV/4, (w & 3 + 1) DV/4): it computes S^T = K Q^T for its 16
-// heads with v_mfma_f32_16x16x32 (the 4 waves of a head group duplicate this small
-// product rather than exchanging P), fp32 softmax with exp2 and deferred rescale, and
-// O^T += V^T P^T with v_mfma_f32_16x16x16 on its DV/4 dims (V^T by ds_read_b64_tr_b16).
+// Workgroup = 4 waves for (split, 32-head group, sequence), two workgroups per CU.
+// 32-key tiles of the shared rows go HBM -> LDS (asm global_load_lds_dwordx4) into a
+// 2-stage ring. Wave w takes heads 16 * (w >> 1) + 0..15 (MFMA columns) and output dims
+// [(w & 1) DV/2, (w & 1 + 1) DV/2): it computes S^T = K Q^T for its 16 heads with
+// v_mfma_f32_16x16x32 (the 2 waves of a head group duplicate this small product rather
+// than exchanging P), fp32 softmax with exp2 and deferred rescale, and O^T += V^T P^T
+// with v_mfma_f32_16x16x16 on its DV/2 dims (V^T by ds_read_b64_tr_b16).
 // Normalised (O, lse) partials per split are merged by decode_combine_kernel.
 // ---------------------------------------------------------------------------------
-constexpr int kMlaWaves = 8;
+constexpr int kMlaWaves = 4;
 constexpr int kMlaThreads = 64 * kMlaWaves;
 constexpr int kMlaTile = 32;
-constexpr int kMlaStages = 3;
+constexpr int kMlaStages = 2;
 constexpr int kMlaRope = 64;
 constexpr int kMlaMaxSplit = 1024;
 constexpr int kMlaDefaultSplit = 512;
@@ -486,16 +486,16 @@ __device__ inline int mla_page_of(const MlaParams& p, int tok, int& slot) {
 __device__ inline int mla_swz(int r) { return (r >> 1) & 7; }
 
 template <typename Tag, int DV>
-__global__ __launch_bounds__(kMlaThreads, 1) void mla_decode_split_kernel(const MlaParams p) {
+__global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const MlaParams p) {
   using E = Elem<Tag>;
   constexpr int DQK = DV + kMlaRope;
   constexpr int CH = DQK / 8;                  // 16-byte chunks per row
   constexpr int TILE = kMlaTile * DQK;         // elements per tile
-  constexpr int LPT = kMlaTile * CH / 256;     // loads per issuing lane per tile
+  constexpr int LPT = kMlaTile * CH / kMlaThreads;  // loads per lane per tile
   constexpr int KS = DQK / 32;                 // QK k-steps
-  constexpr int DW = DV / 4;                   // output dims per wave
+  constexpr int DW = DV / 2;                   // output dims per wave
   constexpr int DBW = DW / 16;                 // 16-dim output blocks per wave
-  static_assert(CH % 8 == 0 && kMlaTile * CH % 256 == 0, "row / tile shape");
+  static_assert(CH % 8 == 0 && kMlaTile * CH % kMlaThreads == 0, "row / tile shape");
   __shared__ __attribute__((aligned(1024))) uint16_t ring[kMlaStages][TILE];
   __shared__ int bt_lds[kMlaMaxSplit + 2];
 
@@ -512,11 +512,10 @@ __global__ __launch_bounds__(kMlaThreads, 1) void mla_decode_split_kernel(const 
   const int lane = tid & 63;
   const int c16 = lane & 15;
   const int g4 = lane >> 4;
-  const int hs = wave >> 2;  // head subgroup: MFMA columns = heads 16 hs + c16
-  const int dq = wave & 3;   // output dim quarter
+  const int hs = wave >> 1;  // head subgroup: MFMA columns = heads 16 hs + c16
+  const int dq = wave & 1;   // output dim half
   const int head = hg * 32 + hs * 16 + c16;
   const bool head_live = head < p.Hq;
-  const bool issuer = wave < 4;
 
   int slot0;
   const int pg0 = mla_page_of(p, s_begin, slot0);
@@ -545,7 +544,7 @@ __global__ __launch_bounds__(kMlaThreads, 1) void mla_decode_split_kernel(const 
 
   const char* pool = reinterpret_cast<const char*>(p.kv);
   const int n_tiles = (s_end - s_begin + kMlaTile - 1) / kMlaTile;
-  // Issuing lanes: load j fills chunk position P = (4j + wave) * 64 + lane of a tile.
+  // Load j of this lane fills chunk position P = (4j + wave) * 64 + lane of a tile.
   auto issue = [&](int t, int st) {
     const int t0 = s_begin + t * kMlaTile;
     uint16_t* dst = ring[st];
@@ -647,21 +646,20 @@ __global__ __launch_bounds__(kMlaThreads, 1) void mla_decode_split_kernel(const 
     }
   };
 
-  if (issuer) {
-    issue(0, 0);
-    if (n_tiles > 1) issue(1, 1);
-  }
+  issue(0, 0);
+  if (n_tiles > 1) issue(1, 1);
   for (int t = 0; t < n_tiles; ++t) {
-    if (issuer) {
-      if (t + 1 < n_tiles) {
-        wait_vmcnt<LPT>();
-      } else {
-        wait_vmcnt0();
-      }
+    if (t + 1 < n_tiles) {
+      wait_vmcnt<LPT>();
+    } else {
+      wait_vmcnt0();
     }
-    __syncthreads();  // tile t is in LDS; every wave is done with tile t-1
-    if (issuer && t + 2 < n_tiles) issue(t + 2, (t + 2) % kMlaStages);
-    compute(t, ring[t % kMlaStages]);
+    __syncthreads();  // tile t is in LDS
+    compute(t, ring[t & 1]);
+    if (t + 2 < n_tiles) {
+      __syncthreads();  // every wave is done with stage t & 1
+      issue(t + 2, t & 1);
+    }
   }
 
   // Partial of this split: O^T lane layout dims 16 db + 4 g4 + j (of this wave's
