@@ -26,6 +26,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from ..kernels import _lib
+from .attention_forward import _positive_scale
 
 
 def _auto_tokens_per_split(batch: int, heads_kv: int, max_len: int) -> int:
@@ -114,6 +115,7 @@ def fastest_flash_paged_decode(
         raise ValueError("block_tables has fewer columns than max_context_len needs")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    q3, scale = _positive_scale(q3, float(scale))
     if sliding_window is not None and int(sliding_window) <= 0:
         raise ValueError("sliding_window must be positive")
     if softcap is not None and float(softcap) <= 0.0:

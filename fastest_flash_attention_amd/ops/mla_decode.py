@@ -25,6 +25,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from ..kernels import _lib
+from .attention_forward import _positive_scale
 
 MLA_ROPE_DIM = 64
 MLA_LATENT_DIMS = (256, 512)
@@ -95,6 +96,7 @@ def fastest_flash_mla_decode(
         raise ValueError("block_tables has fewer columns than max_context_len needs")
     if tokens_per_split is None:
         tokens_per_split = _auto_mla_tokens_per_split(B, (H + 31) // 32, max_context_len)
+    q, scale = _positive_scale(q, float(scale))
 
     lib = _lib.load()
     out = torch.empty((B, H, dim_v), dtype=q.dtype, device=q.device)

@@ -77,6 +77,7 @@ DECODE = [
     ("g32_colgroups", [70, 300], 32, 1, 128, 16, {}, 64),
     ("fp16", [100, 400], 8, 2, 128, 16, {"softcap": 50.0}, None),
     ("empty_seq", [0, 50], 4, 2, 64, 16, {}, None),
+    ("negative_scale", [50, 300], 8, 2, 128, 16, {"scale": -0.1}, None),
 ]
 
 

@@ -68,6 +68,17 @@ def test_mla_decode_parity(dtype, dim_v, H, page_size, lens, tps):
         assert torch.all(o[i] == 0) and torch.all(torch.isneginf(lse[i]))
 
 
+def test_mla_decode_negative_scale():
+    require_gpu()
+    lens = [200, 31]
+    q, pool, bt, lens_t = _paged_case(8, lens, 16, 512, 32, BF16)
+    say("mla decode negative scale")
+    o, lse = ffa.fastest_flash_mla_decode(q.cuda(), pool.cuda(), bt.cuda(), lens_t.cuda(),
+                                          dim_v=512, scale=-0.05, return_lse=True)
+    ro, rl = omla.paged_absorbed_decode(np32(q), np32(pool), bt.numpy(), lens, 512, -0.05)
+    assert_parity(o, ro, lse, rl, "mla negative scale")
+
+
 def test_mla_decode_page_permutation_invariance():
     require_gpu()
     lens = [300, 17]

@@ -39,6 +39,10 @@ CASES = [
     ("single", 1, 2, 2, 1, 1, 64, {}, BF16),
     ("gqa_window_softcap", 2, 8, 2, 333, 333, 128, {"causal": True, "sliding_window": 100,
                                                     "softcap": 50.0, "num_kv_heads": 2}, BF16),
+    # the kernels need scale > 0; the host maps these exactly (negated q / 1e-30)
+    ("negative_scale", 1, 2, 2, 150, 150, 64, {"causal": True, "scale": -0.2}, BF16),
+    ("negative_scale_softcap", 1, 2, 2, 90, 90, 128, {"softcap": 5.0, "scale": -0.3}, BF16),
+    ("zero_scale", 1, 2, 2, 70, 70, 64, {"causal": True, "scale": 0.0}, BF16),
 ]
 
 
