@@ -1,9 +1,9 @@
-"""fastest_flash_attention_amd — MI355X-native forward attention.
+"""fastest_flash_attention_amd — MI355X-native attention.
 
-Drop-in for the forward hot path of MindIntels/fastest_flash_attention
-(reference __init__.py:40-88): the same functional entry point, modules, config and
-paged KV cache, with the GPU work done by hand-written gfx950 HIP kernels in
-libffa.so (C ABI: include/ffa.h).
+Drop-in for the attention hot path of MindIntels/fastest_flash_attention
+(reference __init__.py:40-88): the same functional entry points (forward, backward,
+autograd function), modules, config and paged KV cache, with the GPU work done by
+hand-written gfx950 HIP kernels in libffa.so (C ABI: include/ffa.h).
 """
 
 from .config import AttentionConfig
@@ -17,6 +17,7 @@ from .ops import (
     create_causal_block_mask,
     create_local_block_mask,
     create_sliding_window_block_mask,
+    fastest_flash_attn_backward,
     fastest_flash_attn_forward,
     fastest_flash_attn_func,
     fastest_flash_mla_decode,
@@ -29,6 +30,7 @@ __version__ = "0.1.0"
 __all__ = [
     "AttentionConfig",
     "fastest_flash_attn_forward",
+    "fastest_flash_attn_backward",
     "fastest_flash_attn_func",
     "FastestFlashAttnFunc",
     "fastest_flash_paged_decode",

@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime before libffa.so)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libffa.so")
 
-FFA_ABI_VERSION = 3
+FFA_ABI_VERSION = 4
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
 FFA_DTYPE_FP32 = 2
@@ -165,6 +165,45 @@ class MlaDecodeArgs(ctypes.Structure):
     ]
 
 
+class AttnBwdArgs(ctypes.Structure):
+    """Mirror of ``ffa_attn_bwd_args``."""
+
+    _fields_ = [
+        ("dout", ctypes.c_void_p),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("dq", ctypes.c_void_p),
+        ("dk", ctypes.c_void_p),
+        ("dv", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("do_stride", _I64x4),
+        ("q_stride", _I64x4),
+        ("k_stride", _I64x4),
+        ("v_stride", _I64x4),
+        ("o_stride", _I64x4),
+        ("dq_stride", _I64x4),
+        ("dk_stride", _I64x4),
+        ("dv_stride", _I64x4),
+        ("lse_stride", _I64x3),
+        ("batch", ctypes.c_int32),
+        ("heads_q", ctypes.c_int32),
+        ("heads_kv", ctypes.c_int32),
+        ("seqlen_q", ctypes.c_int32),
+        ("seqlen_kv", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("q_offset", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("window", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("softcap", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 # Every symbol include/ffa.h declares, with its ctypes signature.
 EXPORTS = {
     "ffa_prefill_fwd": (ctypes.c_int, [ctypes.POINTER(PrefillArgs), ctypes.c_void_p]),
@@ -181,6 +220,10 @@ EXPORTS = {
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],
     ),
     "ffa_mla_decode_fwd": (ctypes.c_int, [ctypes.POINTER(MlaDecodeArgs), ctypes.c_void_p]),
+    "ffa_attn_bwd_workspace_bytes": (
+        ctypes.c_size_t, [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],
+    ),
+    "ffa_attn_bwd": (ctypes.c_int, [ctypes.POINTER(AttnBwdArgs), ctypes.c_void_p]),
     "ffa_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "ffa_abi_version": (ctypes.c_int, []),
 }

@@ -22,7 +22,7 @@ PKG_KERNELS = os.path.dirname(HERE)
 REPO = os.path.dirname(os.path.dirname(PKG_KERNELS))
 INCLUDE = os.path.join(REPO, "include")
 OUT_LIB = os.path.join(PKG_KERNELS, "libffa.so")
-SOURCES = ["ffa_api.hip", "ffa_prefill.hip", "ffa_decode.hip"]
+SOURCES = ["ffa_api.hip", "ffa_prefill.hip", "ffa_decode.hip", "ffa_backward.hip"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 are emitted (scalar fp32 VALU only).

@@ -35,7 +35,7 @@ const char* ffa_strerror(int status) {
     case FFA_ERR_GQA_RATIO:
       return "ffa: heads_q must be a positive multiple of heads_kv";
     case FFA_ERR_WORKSPACE:
-      return "ffa: decode workspace missing or smaller than ffa_paged_decode_workspace_bytes()";
+      return "ffa: workspace missing or smaller than the entry point's *_workspace_bytes()";
     case FFA_ERR_LAUNCH:
       return "ffa: kernel launch failed";
     case FFA_ERR_NO_DEVICE:
@@ -227,6 +227,65 @@ int ffa_mla_decode_fwd(const ffa_mla_decode_args* a, void* stream) {
   if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need)) return FFA_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 15u) != 0) return FFA_ERR_MISALIGNED;
   return ffa::launch_mla_decode(*a, static_cast<hipStream_t>(stream));
+}
+
+size_t ffa_attn_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q) {
+  if (batch < 0 || heads_q < 0 || seqlen_q < 0) return 0;
+  return ffa::attn_bwd_workspace_bytes(batch, heads_q, seqlen_q);
+}
+
+int ffa_attn_bwd(const ffa_attn_bwd_args* a, void* stream) {
+  if (a == nullptr) return FFA_ERR_INVALID_ARG;
+  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (a->head_dim < 1 || a->head_dim > 128) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->seqlen_q < 0 || a->seqlen_kv < 0) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->heads_q % a->heads_kv != 0) return FFA_ERR_GQA_RATIO;
+  if (a->batch == 0 || a->seqlen_q == 0) return FFA_OK;
+  if (a->dout == nullptr || a->q == nullptr || a->o == nullptr || a->lse == nullptr ||
+      a->dq == nullptr) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->seqlen_kv > 0 && (a->k == nullptr || a->v == nullptr || a->dk == nullptr ||
+                           a->dv == nullptr)) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  const int64_t* strides[8] = {a->do_stride, a->q_stride,  a->k_stride,  a->v_stride,
+                               a->o_stride,  a->dq_stride, a->dk_stride, a->dv_stride};
+  for (const int64_t* st : strides) {
+    if (st[3] != 1) return FFA_ERR_INVALID_ARG;
+    for (int i = 0; i < 3; ++i) {
+      if (st[i] < 0) return FFA_ERR_INVALID_ARG;
+    }
+  }
+  for (int i = 0; i < 3; ++i) {
+    if (a->lse_stride[i] < 0) return FFA_ERR_INVALID_ARG;
+  }
+  if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
+  const void* ptrs[8] = {a->dout, a->q, a->k, a->v, a->o, a->dq, a->dk, a->dv};
+  for (const void* ptr : ptrs) {
+    if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) return FFA_ERR_MISALIGNED;
+  }
+  for (const int64_t* st : strides) {
+    for (int i = 0; i < 3; ++i) {
+      if (st[i] % 8 != 0) return FFA_ERR_MISALIGNED;
+    }
+  }
+  // 32-bit byte offsets of rows inside a tile
+  if (a->q_stride[2] >= (int64_t{1} << 24) || a->do_stride[2] >= (int64_t{1} << 24) ||
+      a->k_stride[2] >= (int64_t{1} << 24) || a->v_stride[2] >= (int64_t{1} << 24)) {
+    return FFA_ERR_TOO_LARGE;
+  }
+  const int64_t max_pos = static_cast<int64_t>(a->q_offset) + a->seqlen_q;
+  if (max_pos > 0x3fffffff || a->seqlen_kv > 0x3fffffff || a->q_offset < -0x3fffffff) {
+    return FFA_ERR_TOO_LARGE;
+  }
+  const size_t need = ffa::attn_bwd_workspace_bytes(a->batch, a->heads_q, a->seqlen_q);
+  if (a->workspace == nullptr || a->workspace_bytes < need) return FFA_ERR_WORKSPACE;
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 15u) != 0) return FFA_ERR_MISALIGNED;
+  return ffa::launch_attn_bwd(*a, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

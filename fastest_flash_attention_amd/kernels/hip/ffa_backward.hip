@@ -1,0 +1,764 @@
+// Attention backward (recompute from q, k, v, O, LSE) for gfx950.
+//
+// Semantics follow flash_attn_cpu_backward (reference kernels/cpu_reference.py:319-427):
+//   P    = exp(S - lse)               S = softcap(q.k * scale) with the forward's masks
+//   D_i  = rowsum(dO * O)             (O as stored by the forward, fp32 sum)
+//   dV   = P^T dO
+//   dS   = P * (dO V^T - D_i)         times (1 - tanh^2(q.k * scale / cap)) with softcap
+//   dQ   = scale * dS K,   dK = scale * dS^T Q
+// GQA (q head h reads kv head h / ratio) is reduced inside the kernel: dK / dV of a KV
+// head sum over the q heads of its group. A row whose LSE is -inf (no visible key in
+// the two-pass forward) contributes nothing (P = 0).
+//
+// Three launches on the caller's stream, no atomics (results are run-to-run
+// deterministic):
+//   1. bwd_pre_kernel   lse2 = lse * log2e (+inf for -inf rows and the padding rows up
+//                       to the next 128-row boundary) and D_i, both fp32, into the
+//                       workspace [B * Hq][Sq_pad].
+//   2. bwd_dkdv_kernel  keys stationary: one workgroup (4 waves) per 128 keys of one
+//                       (batch, kv head); each wave holds 32 keys' K and V rows as MFMA
+//                       B operands and their dK^T / dV^T accumulators in registers, and
+//                       sweeps 32-row tiles of Q, dO, lse2, D_i of every q head of its
+//                       group (direct global -> LDS loads, double-buffered):
+//                         S  = Q K^T, dP = dO V^T      lane l holds key l % 32
+//                         dV^T += dO^T P, dK^T += Q^T dS   A = ds_read_b64_tr_b16 of the
+//                         Q / dO tile, B = P / dS packed from the accumulators
+//   3. bwd_dq_kernel    queries stationary: one workgroup per 128 query rows of one
+//                       (batch, q head), the forward kernel's decomposition; per 64-key
+//                       tile S^T = K Q^T, dP^T = V dO^T (lane = query, lse2 / D_i in
+//                       one register each), dQ^T += K^T dS^T with K^T transposed-read
+//                       from the same LDS tile.
+// The Q / dO (kernel 2) and K (kernel 3) tiles are read both row-wise (MFMA A rows)
+// and transposed; one XOR swizzle of the 16-byte chunk index keeps both access forms
+// free of LDS bank conflicts.
+// P and dS are rounded to the input's 16-bit type for the MFMAs; everything else is
+// fp32. Inputs are 16-byte aligned with head_dim % 8 == 0 (the host pads otherwise);
+// head_dim up to 128.
+
+#include "ffa_common.h"
+#include "ffa_internal.h"
+
+namespace ffa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kQTile = 128;   // q rows per dQ workgroup, and the Sq padding unit
+constexpr int kKeyTile = 64;  // keys per dQ k-tile
+constexpr int kDkvKeys = 128; // keys per dK/dV workgroup
+constexpr int kDkvRows = 32;  // q rows per dK/dV tile
+
+struct BwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;
+  const uint16_t* dout;
+  const float* lse;
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  float* lse2;  // workspace [B * Hq][sq_pad]
+  float* di;    // workspace [B * Hq][sq_pad]
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  int64_t do_sb, do_sh, do_ss;
+  int64_t dq_sb, dq_sh, dq_ss;
+  int64_t dk_sb, dk_sh, dk_ss;
+  int64_t dv_sb, dv_sh, dv_ss;
+  int64_t l_sb, l_sh, l_ss;
+  int B, Hq, Hkv, Sq, Skv, D;
+  int q_offset, causal, window;
+  int ratio;
+  int sq_pad;
+  int n_qt;        // dQ workgroups per (batch, q head)
+  int n_kt;        // dK/dV workgroups per (batch, kv head)
+  float score_mul; // scale*log2e, or scale/softcap with softcap
+  float cap_mul;   // softcap*log2e
+  float tanh_mul;  // 2*log2e*scale/softcap: tanh(x) = 1 - 2 / (1 + exp2(q.k * tanh_mul))
+  float scale;
+  int xcd_remap_dq, xcd_remap_dkv;
+};
+
+// XOR swizzle of the 16-byte chunk index of tile row r. Row-wise MFMA operand reads
+// (16 lanes, 16 rows, one chunk each) need r -> swz(r) injective over 16 rows (within
+// one row parity for 128-byte rows); ds_read_b64_tr_b16 (rows r0..r0+3, r0 % 4 == 0,
+// 4 consecutive chunks) needs swz(r) >> 2 distinct over those 4 rows (128-byte rows:
+// rows of one parity distinct). swz(r + 16) == swz(r) for both widths.
+template <int DP>
+__device__ inline int bswz(int r) {
+  if constexpr (DP == 128) {
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+  } else {
+    const int s = (r >> 1) & 7;
+    return ((s & 1) << 2) | (s >> 1);
+  }
+}
+
+template <int DP>
+struct BShape {
+  static constexpr int CPR = DP / 8;  // 16-byte chunks per row
+  static constexpr int KS = DP / 16;  // MFMA k-steps over the head dim
+  static constexpr int DB = DP / 32;  // 32-dim output blocks
+};
+
+// Row `row` of a [*, DP] tile as the MFMA register operand of k-step ks: dims
+// 16 ks + 8 g .. +7, zero at and beyond D.
+template <int DP>
+__device__ inline void load_row_operand(const uint16_t* row, int D, int g,
+                                        u32x4 (&reg)[BShape<DP>::KS]) {
+#pragma unroll
+  for (int ks = 0; ks < BShape<DP>::KS; ++ks) {
+    const int d0 = min(16 * ks + 8 * g, D - 8);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(row + d0);
+    reg[ks] = (16 * ks + 8 * g < D) ? v : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// Store one 32-row block of MFMA accumulators (lane l32 = row, dims 32 db + 8 i + 4 g + j)
+// times `mul` as 16-bit elements.
+template <typename Tag, int DP>
+__device__ inline void store_rows(uint16_t* row, const f32x16 (&acc)[BShape<DP>::DB], float mul,
+                                  int D, int g) {
+  using E = Elem<Tag>;
+#pragma unroll
+  for (int db = 0; db < BShape<DP>::DB; ++db) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = 32 * db + 8 * i + 4 * g;
+      const uint32_t w0 = E::pack2(acc[db][4 * i + 0] * mul, acc[db][4 * i + 1] * mul);
+      const uint32_t w1 = E::pack2(acc[db][4 * i + 2] * mul, acc[db][4 * i + 3] * mul);
+      if (d0 < D) *reinterpret_cast<u32x2*>(row + d0) = u32x2{w0, w1};
+    }
+  }
+}
+
+// Element offsets inside a swizzled [rows, DP] tile are row * DP | chunk << 3 | elem,
+// with disjoint bit fields, so moving to chunk c ^ m is an XOR of the offset with
+// m << 3: one base offset per lane serves every k-step and dim block (the per-step
+// offsets are not held in registers).
+//
+// Row-wise A operand of k-step ks: tile row l32, chunk 2 ks + g.
+template <int DP>
+__device__ inline int row_rd0(int lane) {
+  const int l32 = lane & 31;
+  return l32 * DP + ((((lane >> 5)) ^ bswz<DP>(l32)) << 3);
+}
+__device__ inline int row_rd(int base, int ks) { return base ^ (ks << 4); }
+
+// The two ds_read_b64_tr_b16 reads (rows 4g + 0..3 and 8 + 4g + 0..3 of a 16-row chunk;
+// dims colw .. colw + 3 of a 32-dim block) that form the A operand [32 dims x 16 rows]
+// of dims 32 db .. +31 are at base ^ (db << 5). The row order they produce is the row
+// order an accumulator's lane half holds in elements 8c .. 8c + 7.
+template <int DP>
+__device__ inline void tr_offsets(int lane, int& lo, int& hi) {
+  const int g = lane >> 5;
+  const int rowoff = 4 * g + ((lane & 15) >> 2);
+  const int colw = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int cg = colw >> 3;
+  lo = rowoff * DP + ((cg ^ bswz<DP>(rowoff)) << 3) + (colw & 7);
+  hi = (rowoff + 8) * DP + ((cg ^ bswz<DP>(rowoff + 8)) << 3) + (colw & 7);
+}
+
+// Hide a value's origin from the optimizer: the offsets derived from it inside a
+// loop are recomputed there (one XOR each) instead of being hoisted into registers.
+__device__ inline int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+__device__ inline u32x4 tr_operand(const uint16_t* tile, int lo, int hi, int db) {
+  const u32x2 a = lds_read_tr16(tile + (lo ^ (db << 5)));
+  const u32x2 b = lds_read_tr16(tile + (hi ^ (db << 5)));
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// ---------------------------------------------------------------------------------
+// 1. lse2 and D_i. 32 rows per workgroup, 8 lanes per row.
+// ---------------------------------------------------------------------------------
+template <typename Tag>
+__global__ __launch_bounds__(kThreads) void bwd_pre_kernel(const BwdParams p) {
+  using E = Elem<Tag>;
+  const int tid = threadIdx.x;
+  const int part = tid & 7;
+  const int64_t rg = static_cast<int64_t>(blockIdx.x) * 32 + (tid >> 3);  // < B*Hq*sq_pad
+  const int bh = static_cast<int>(rg / p.sq_pad);
+  const int s = static_cast<int>(rg - static_cast<int64_t>(bh) * p.sq_pad);
+  const int b = bh / p.Hq;
+  const int h = bh - b * p.Hq;
+  float acc = 0.0f;
+  if (s < p.Sq) {
+    const uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(s) * p.o_ss;
+    const uint16_t* drow = p.dout + b * p.do_sb + h * p.do_sh + static_cast<int64_t>(s) * p.do_ss;
+    for (int c = part; c < (p.D >> 3); c += 8) {
+      const u32x4 ov = *reinterpret_cast<const u32x4*>(orow + 8 * c);
+      const u32x4 dv = *reinterpret_cast<const u32x4*>(drow + 8 * c);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        acc = fmaf(E::to_f32(static_cast<uint16_t>(ov[w] & 0xffffu)),
+                   E::to_f32(static_cast<uint16_t>(dv[w] & 0xffffu)), acc);
+        acc = fmaf(E::to_f32(static_cast<uint16_t>(ov[w] >> 16)),
+                   E::to_f32(static_cast<uint16_t>(dv[w] >> 16)), acc);
+      }
+    }
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  if (part == 0) {
+    float l2 = __builtin_inff();
+    float di = 0.0f;
+    if (s < p.Sq) {
+      const float l = p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(s) * p.l_ss];
+      l2 = (l == kNegInf) ? __builtin_inff() : l * kLog2e;
+      di = acc;
+    }
+    p.lse2[rg] = l2;
+    p.di[rg] = di;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 2. dK, dV: keys stationary.
+// ---------------------------------------------------------------------------------
+template <typename Tag, int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p) {
+  using S = BShape<DP>;
+  using E = Elem<Tag>;
+  constexpr int TILE = kDkvRows * DP;
+  constexpr int LPT = kDkvRows * S::CPR / kThreads;  // tile loads per thread per tensor
+  static_assert(kDkvRows * S::CPR % kThreads == 0, "tile must split evenly");
+  __shared__ __attribute__((aligned(1024))) uint16_t q_lds[2][TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t do_lds[2][TILE];
+  __shared__ __attribute__((aligned(1024))) float st_lds[2][256];  // [0,32) lse2, [32,64) D_i
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[4][32 * DP];  // each wave's V rows
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  int bid = blockIdx.x;
+  if (p.xcd_remap_dkv) {
+    const int per_xcd = gridDim.x >> 3;
+    bid = (bid & 7) * per_xcd + (bid >> 3);
+  }
+  const int bh = bid / p.n_kt;
+  const int kt = bid - bh * p.n_kt;  // causal: low key tiles are seen by the most rows
+  const int b = bh / p.Hkv;
+  const int hk = bh - b * p.Hkv;
+  const int D = p.D;
+  const int Sq = p.Sq;
+
+  const int k0 = kt * kDkvKeys;
+  const int kw0 = k0 + wave * 32;
+  const int key = kw0 + l32;
+  const bool wave_live = kw0 < p.Skv;
+  const int k_last = min(k0 + kDkvKeys, p.Skv) - 1;
+
+  // q rows whose visible keys meet [k0, k_last]: causal q_abs >= key, window
+  // q_abs <= key + window - 1.
+  const int q_lo = p.causal ? max(0, k0 - p.q_offset) : 0;
+  const int q_hi = p.window > 0
+                       ? static_cast<int>(min<int64_t>(Sq, static_cast<int64_t>(k_last) + p.window -
+                                                               p.q_offset))
+                       : Sq;
+  const int qt_begin = q_lo / kDkvRows;
+  const int ntq = q_hi > q_lo ? (q_hi + kDkvRows - 1) / kDkvRows - qt_begin : 0;
+  const int nit = ntq * p.ratio;
+
+  const float c = SOFTCAP ? p.cap_mul : p.score_mul;
+
+  // K row of this lane's key as the B operand of S (clamped row; keys >= Skv are never
+  // stored). The wave's 32 V rows go to its own LDS slice (swizzled like the tiles) and
+  // are read back as the B operand of dP: registers for both would not fit. Dims at and
+  // beyond D are zero in the slice (the dO tile's padding dims are not).
+  const int dchunks = D >> 3;
+  u32x4 kreg[S::KS];
+  load_row_operand<DP>(p.k + b * p.k_sb + hk * p.k_sh +
+                           static_cast<int64_t>(min(key, p.Skv - 1)) * p.k_ss, D, g, kreg);
+  if (wave_live) {
+    const uint16_t* vb = p.v + b * p.v_sb + hk * p.v_sh + static_cast<int64_t>(kw0) * p.v_ss;
+#pragma unroll
+    for (int j = 0; j < 32 * S::CPR / 64; ++j) {
+      const int pos = j * 64 + lane;
+      const int row = pos / S::CPR;
+      const int cq = (pos - row * S::CPR) ^ bswz<DP>(row);
+      const int rr = min(row, p.Skv - 1 - kw0);
+      u32x4 val = {0u, 0u, 0u, 0u};
+      if (cq < dchunks) val = *reinterpret_cast<const u32x4*>(vb + static_cast<int64_t>(rr) * p.v_ss + 8 * cq);
+      *reinterpret_cast<u32x4*>(&v_lds[wave][8 * pos]) = val;
+    }
+  }
+  const uint16_t* vw = v_lds[wave];
+
+  // Tile loads: load j of this thread fills chunk position P = (4j + wave) * 64 + lane;
+  // LDS (row, c) holds global chunk c ^ bswz(row), clamped below head_dim.
+  uint32_t q_off[LPT], do_off[LPT];
+#pragma unroll
+  for (int j = 0; j < LPT; ++j) {
+    const int pos = (4 * j + wave) * 64 + lane;
+    const int row = pos / S::CPR;
+    const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
+    q_off[j] = static_cast<uint32_t>(row * p.q_ss * 2 + cq * 16);
+    do_off[j] = static_cast<uint32_t>(row * p.do_ss * 2 + cq * 16);
+  }
+  auto issue = [&](int it, int buf) {
+    const int hq = hk * p.ratio + it / ntq;
+    const int q0 = (qt_begin + it % ntq) * kDkvRows;
+    const char* qb = reinterpret_cast<const char*>(p.q + b * p.q_sb + hq * p.q_sh +
+                                                   static_cast<int64_t>(q0) * p.q_ss);
+    const char* db = reinterpret_cast<const char*>(p.dout + b * p.do_sb + hq * p.do_sh +
+                                                   static_cast<int64_t>(q0) * p.do_ss);
+    if (q0 + kDkvRows <= Sq) {
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        load_lds16_async(qb, q_off[j], lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(db, do_off[j], lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+      }
+    } else {
+      // rows past Sq re-read row Sq - 1: their lse2 is +inf, so P = dS = 0
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        const int row = ((4 * j + wave) * 64 + lane) / S::CPR;
+        const int over = max(0, q0 + row - (Sq - 1));
+        const uint32_t qback = static_cast<uint32_t>(over * p.q_ss * 2);
+        const uint32_t dback = static_cast<uint32_t>(over * p.do_ss * 2);
+        load_lds16_async(qb, q_off[j] - qback, lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(db, do_off[j] - dback, lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+      }
+    }
+    if (wave == 0) {
+      // lanes 0-7: lse2 rows q0 .. q0+31, lanes 8-15: D_i; the other lanes repeat them
+      // into the unused rest of the 1 KiB stats buffer
+      const int64_t ws = (static_cast<int64_t>(b) * p.Hq + hq) * p.sq_pad + q0 + 4 * (lane & 7);
+      const float* src = ((lane & 8) ? p.di : p.lse2) + ws;
+      load_lds16_async(src, lds_addr(&st_lds[buf][0]));
+    }
+  };
+
+  const int a_rd0 = row_rd0<DP>(lane);
+  int t_lo0, t_hi0;
+  tr_offsets<DP>(lane, t_lo0, t_hi0);
+
+  f32x16 dkacc[S::DB], dvacc[S::DB];
+#pragma unroll
+  for (int db = 0; db < S::DB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dkacc[db][r] = 0.0f;
+      dvacc[db][r] = 0.0f;
+    }
+  }
+
+  if (nit > 0) issue(0, 0);
+  for (int it = 0; it < nit; ++it) {
+    const int buf = it & 1;
+    wait_vmcnt0();
+    __syncthreads();
+    if (it + 1 < nit) issue(it + 1, buf ^ 1);
+    const int q0 = (qt_begin + it % ntq) * kDkvRows;
+    const int q0_abs = p.q_offset + q0;
+    if (!wave_live) continue;
+    if (p.causal && kw0 > q0_abs + kDkvRows - 1) continue;
+    if (p.window > 0 && kw0 + 31 < q0_abs - p.window + 1) continue;
+    const uint16_t* ql = q_lds[buf];
+    const uint16_t* dl = do_lds[buf];
+    const float* st = st_lds[buf];
+    const int a_rd = opaque(a_rd0);
+    const int t_lo = opaque(t_lo0);
+    const int t_hi = opaque(t_hi0);
+
+    f32x16 sacc, dpacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = 0.0f;
+      dpacc[r] = 0.0f;
+    }
+#pragma unroll
+    for (int ks = 0; ks < S::KS; ++ks) {
+      const u32x4 aq = *reinterpret_cast<const u32x4*>(ql + row_rd(a_rd, ks));
+      const u32x4 ad = *reinterpret_cast<const u32x4*>(dl + row_rd(a_rd, ks));
+      const u32x4 bv = *reinterpret_cast<const u32x4*>(vw + row_rd(a_rd, ks));
+      sacc = E::mfma32(aq, kreg[ks], sacc);
+      dpacc = E::mfma32(ad, bv, dpacc);
+    }
+
+    // element (row 8i + 4g + j, key l32) sits in accumulator 4i + j
+    const bool need_mask = (p.causal && kw0 + 31 > q0_abs) ||
+                           (p.window > 0 && kw0 < q0_abs + kDkvRows - 1 - p.window + 1);
+    float pv[16], dsv[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 l2 = *reinterpret_cast<const f32x4*>(st + 8 * i + 4 * g);
+      const f32x4 di = *reinterpret_cast<const f32x4*>(st + 32 + 8 * i + 4 * g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * i + j;
+        if constexpr (SOFTCAP) {
+          const float t = tanh_fast(sacc[r] * p.tanh_mul);
+          pv[r] = fast_exp2(fmaf(t, c, -l2[j]));
+          dsv[r] = pv[r] * (dpacc[r] - di[j]) * fmaf(-t, t, 1.0f);
+        } else {
+          pv[r] = fast_exp2(fmaf(sacc[r], c, -l2[j]));
+          dsv[r] = pv[r] * (dpacc[r] - di[j]);
+        }
+      }
+    }
+    if (need_mask) {
+      const int qa0 = q0_abs + 4 * g;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qa = qa0 + 8 * (r >> 2) + (r & 3);
+        const bool ok = (!p.causal || key <= qa) && (p.window <= 0 || key >= qa - p.window + 1);
+        pv[r] = ok ? pv[r] : 0.0f;
+        dsv[r] = ok ? dsv[r] : 0.0f;
+      }
+    }
+    // dV^T[d, key] += dO^T[d, row] P[row, key]; dK^T[d, key] += Q^T[d, row] dS[row, key]
+#pragma unroll
+    for (int cc = 0; cc < 2; ++cc) {
+      const int e0 = 8 * cc;
+      const u32x4 bp = {E::pack2(pv[e0 + 0], pv[e0 + 1]), E::pack2(pv[e0 + 2], pv[e0 + 3]),
+                        E::pack2(pv[e0 + 4], pv[e0 + 5]), E::pack2(pv[e0 + 6], pv[e0 + 7])};
+      const u32x4 bs = {E::pack2(dsv[e0 + 0], dsv[e0 + 1]), E::pack2(dsv[e0 + 2], dsv[e0 + 3]),
+                        E::pack2(dsv[e0 + 4], dsv[e0 + 5]), E::pack2(dsv[e0 + 6], dsv[e0 + 7])};
+#pragma unroll
+      for (int db = 0; db < S::DB; ++db) {
+        const u32x4 ado = tr_operand(dl + 16 * cc * DP, t_lo, t_hi, db);
+        const u32x4 aq = tr_operand(ql + 16 * cc * DP, t_lo, t_hi, db);
+        dvacc[db] = E::mfma32(ado, bp, dvacc[db]);
+        dkacc[db] = E::mfma32(aq, bs, dkacc[db]);
+      }
+    }
+  }
+
+  if (wave_live && key < p.Skv) {
+    store_rows<Tag, DP>(p.dk + b * p.dk_sb + hk * p.dk_sh + static_cast<int64_t>(key) * p.dk_ss,
+                        dkacc, p.scale, D, g);
+    store_rows<Tag, DP>(p.dv + b * p.dv_sb + hk * p.dv_sh + static_cast<int64_t>(key) * p.dv_ss,
+                        dvacc, 1.0f, D, g);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// 3. dQ: queries stationary.
+// ---------------------------------------------------------------------------------
+template <typename Tag, int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(const BwdParams p) {
+  using S = BShape<DP>;
+  using E = Elem<Tag>;
+  constexpr int BN = kKeyTile;
+  constexpr int TILE = BN * DP;
+  constexpr int LPT = BN * S::CPR / kThreads;
+  static_assert(BN * S::CPR % kThreads == 0, "tile must split evenly");
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][TILE];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  int bid = blockIdx.x;
+  if (p.xcd_remap_dq) {
+    const int per_xcd = gridDim.x >> 3;
+    bid = (bid & 7) * per_xcd + (bid >> 3);
+  }
+  const int bh = bid / p.n_qt;
+  const int jq = bid - bh * p.n_qt;
+  const int qt = p.causal ? (p.n_qt - 1 - jq) : jq;
+  const int b = bh / p.Hq;
+  const int h = bh - b * p.Hq;
+  const int hk = h / p.ratio;
+  const int D = p.D;
+  const int Skv = p.Skv;
+
+  const int q0 = qt * kQTile;
+  const int q_last = min(q0 + kQTile, p.Sq) - 1;
+  const int q0_abs = p.q_offset + q0;
+  const int ql_abs = p.q_offset + q_last;
+  const int kv_lo = p.window > 0 ? max(0, q0_abs - p.window + 1) : 0;
+  const int kv_hi = p.causal ? min(Skv, ql_abs + 1) : Skv;
+  const int t_begin = kv_lo / BN;
+  const int nt = kv_hi > kv_lo ? (kv_hi + BN - 1) / BN - t_begin : 0;
+
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + l32;
+  const bool wave_live = qw0 < p.Sq;
+  const int qw0_abs = p.q_offset + qw0;
+  const int qwl_abs = p.q_offset + min(qw0 + 31, p.Sq - 1);
+  const int qa = p.q_offset + qrow;
+
+  const float c = SOFTCAP ? p.cap_mul : p.score_mul;
+  // this lane's row statistics (padding rows: lse2 = +inf, D_i = 0)
+  const int64_t ws = static_cast<int64_t>(bh) * p.sq_pad + qrow;
+  const float lse2 = p.lse2[ws];
+  const float di = p.di[ws];
+
+  u32x4 qreg[S::KS], doreg[S::KS];
+  {
+    const int qr = min(qrow, p.Sq - 1);
+    load_row_operand<DP>(p.q + b * p.q_sb + h * p.q_sh + static_cast<int64_t>(qr) * p.q_ss, D, g, qreg);
+    load_row_operand<DP>(p.dout + b * p.do_sb + h * p.do_sh + static_cast<int64_t>(qr) * p.do_ss, D, g,
+                         doreg);
+  }
+
+  const char* kbytes = reinterpret_cast<const char*>(p.k + b * p.k_sb + hk * p.k_sh);
+  const char* vbytes = reinterpret_cast<const char*>(p.v + b * p.v_sb + hk * p.v_sh);
+  const int dchunks = D >> 3;
+  uint32_t k_off[LPT], v_off[LPT];
+#pragma unroll
+  for (int j = 0; j < LPT; ++j) {
+    const int pos = (4 * j + wave) * 64 + lane;
+    const int row = pos / S::CPR;
+    const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
+    k_off[j] = static_cast<uint32_t>(row * p.k_ss * 2 + cq * 16);
+    v_off[j] = static_cast<uint32_t>(row * p.v_ss * 2 + cq * 16);
+  }
+  auto issue = [&](int t, int buf) {
+    const int kt0 = t * BN;
+    const char* kb = kbytes + static_cast<int64_t>(kt0) * p.k_ss * 2;
+    const char* vb = vbytes + static_cast<int64_t>(kt0) * p.v_ss * 2;
+    if (kt0 + BN <= Skv) {
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        load_lds16_async(kb, k_off[j], lds_addr(&k_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(vb, v_off[j], lds_addr(&v_lds[buf][(4 * j + wave) * 512]));
+      }
+    } else {
+      // rows past Skv re-read row Skv - 1 (masked below)
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        const int row = ((4 * j + wave) * 64 + lane) / S::CPR;
+        const int over = max(0, kt0 + row - (Skv - 1));
+        load_lds16_async(kb, k_off[j] - static_cast<uint32_t>(over * p.k_ss * 2),
+                         lds_addr(&k_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(vb, v_off[j] - static_cast<uint32_t>(over * p.v_ss * 2),
+                         lds_addr(&v_lds[buf][(4 * j + wave) * 512]));
+      }
+    }
+  };
+
+  const int a_rd0 = row_rd0<DP>(lane);
+  int t_lo0, t_hi0;
+  tr_offsets<DP>(lane, t_lo0, t_hi0);
+
+  f32x16 dqacc[S::DB];
+#pragma unroll
+  for (int db = 0; db < S::DB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dqacc[db][r] = 0.0f;
+  }
+
+  if (nt > 0) issue(t_begin, 0);
+  for (int i = 0; i < nt; ++i) {
+    const int buf = i & 1;
+    const int t = t_begin + i;
+    const int kt0 = t * BN;
+    wait_vmcnt0();
+    __syncthreads();
+    if (i + 1 < nt) issue(t + 1, buf ^ 1);
+    if (!wave_live) continue;
+    if (p.causal && kt0 > qwl_abs) continue;
+    const uint16_t* kl = k_lds[buf];
+    const uint16_t* vl = v_lds[buf];
+    const int a_rd = opaque(a_rd0);
+    const int t_lo = opaque(t_lo0);
+    const int t_hi = opaque(t_hi0);
+
+    f32x16 sacc[2], dpacc[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sacc[nb][r] = 0.0f;
+        dpacc[nb][r] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < S::KS; ++ks) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const u32x4 ak = *reinterpret_cast<const u32x4*>(kl + row_rd(a_rd, ks) + nb * 32 * DP);
+        const u32x4 av = *reinterpret_cast<const u32x4*>(vl + row_rd(a_rd, ks) + nb * 32 * DP);
+        sacc[nb] = E::mfma32(ak, qreg[ks], sacc[nb]);
+        dpacc[nb] = E::mfma32(av, doreg[ks], dpacc[nb]);
+      }
+    }
+
+    // element (key 32 nb + 8 i + 4 g + j, query l32) sits in sacc[nb][4i + j]
+    const bool need_mask = (kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
+                           (p.window > 0 && kt0 < qwl_abs - p.window + 1);
+    float dsv[2][16];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (SOFTCAP) {
+          const float tt = tanh_fast(sacc[nb][r] * p.tanh_mul);
+          dsv[nb][r] = fast_exp2(fmaf(tt, c, -lse2)) * (dpacc[nb][r] - di) * fmaf(-tt, tt, 1.0f);
+        } else {
+          dsv[nb][r] = fast_exp2(fmaf(sacc[nb][r], c, -lse2)) * (dpacc[nb][r] - di);
+        }
+      }
+    }
+    if (need_mask) {
+      const int key0 = kt0 + 4 * g;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = key0 + 32 * nb + 8 * (r >> 2) + (r & 3);
+          const bool ok = kk < Skv && (!p.causal || kk <= qa) &&
+                          (p.window <= 0 || kk >= qa - p.window + 1);
+          dsv[nb][r] = ok ? dsv[nb][r] : 0.0f;
+        }
+      }
+    }
+    // dQ^T[d, q] += K^T[d, key] dS^T[key, q]
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const int nb = cc >> 1;
+      const int e0 = (cc & 1) * 8;
+      const u32x4 bs = {E::pack2(dsv[nb][e0 + 0], dsv[nb][e0 + 1]),
+                        E::pack2(dsv[nb][e0 + 2], dsv[nb][e0 + 3]),
+                        E::pack2(dsv[nb][e0 + 4], dsv[nb][e0 + 5]),
+                        E::pack2(dsv[nb][e0 + 6], dsv[nb][e0 + 7])};
+#pragma unroll
+      for (int db = 0; db < S::DB; ++db) {
+        const u32x4 ak = tr_operand(kl + 16 * cc * DP, t_lo, t_hi, db);
+        dqacc[db] = E::mfma32(ak, bs, dqacc[db]);
+      }
+    }
+  }
+
+  if (wave_live && qrow < p.Sq) {
+    store_rows<Tag, DP>(p.dq + b * p.dq_sb + h * p.dq_sh + static_cast<int64_t>(qrow) * p.dq_ss,
+                        dqacc, p.scale, D, g);
+  }
+}
+
+template <typename Tag, int DP, bool SOFTCAP>
+void launch_main(const BwdParams& p, int grid_dkv, int grid_dq, hipStream_t s) {
+  if (grid_dkv > 0) {
+    hipLaunchKernelGGL((bwd_dkdv_kernel<Tag, DP, SOFTCAP>), dim3(grid_dkv), dim3(kThreads), 0, s, p);
+  }
+  hipLaunchKernelGGL((bwd_dq_kernel<Tag, DP, SOFTCAP>), dim3(grid_dq), dim3(kThreads), 0, s, p);
+}
+
+template <typename Tag>
+void launch_tag(const BwdParams& p, bool softcap, int grid_pre, int grid_dkv, int grid_dq,
+                hipStream_t s) {
+  hipLaunchKernelGGL((bwd_pre_kernel<Tag>), dim3(grid_pre), dim3(kThreads), 0, s, p);
+  if (p.D <= 64) {
+    softcap ? launch_main<Tag, 64, true>(p, grid_dkv, grid_dq, s)
+            : launch_main<Tag, 64, false>(p, grid_dkv, grid_dq, s);
+  } else {
+    softcap ? launch_main<Tag, 128, true>(p, grid_dkv, grid_dq, s)
+            : launch_main<Tag, 128, false>(p, grid_dkv, grid_dq, s);
+  }
+}
+
+int64_t sq_padded(int32_t seqlen_q) {
+  return (static_cast<int64_t>(seqlen_q) + kQTile - 1) / kQTile * kQTile;
+}
+
+}  // namespace
+
+size_t attn_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q) {
+  return static_cast<size_t>(2) * batch * heads_q * sq_padded(seqlen_q) * sizeof(float);
+}
+
+int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream) {
+  BwdParams p{};
+  p.q = static_cast<const uint16_t*>(a.q);
+  p.k = static_cast<const uint16_t*>(a.k);
+  p.v = static_cast<const uint16_t*>(a.v);
+  p.o = static_cast<const uint16_t*>(a.o);
+  p.dout = static_cast<const uint16_t*>(a.dout);
+  p.lse = a.lse;
+  p.dq = static_cast<uint16_t*>(a.dq);
+  p.dk = static_cast<uint16_t*>(a.dk);
+  p.dv = static_cast<uint16_t*>(a.dv);
+  p.q_sb = a.q_stride[0];
+  p.q_sh = a.q_stride[1];
+  p.q_ss = a.q_stride[2];
+  p.k_sb = a.k_stride[0];
+  p.k_sh = a.k_stride[1];
+  p.k_ss = a.k_stride[2];
+  p.v_sb = a.v_stride[0];
+  p.v_sh = a.v_stride[1];
+  p.v_ss = a.v_stride[2];
+  p.o_sb = a.o_stride[0];
+  p.o_sh = a.o_stride[1];
+  p.o_ss = a.o_stride[2];
+  p.do_sb = a.do_stride[0];
+  p.do_sh = a.do_stride[1];
+  p.do_ss = a.do_stride[2];
+  p.dq_sb = a.dq_stride[0];
+  p.dq_sh = a.dq_stride[1];
+  p.dq_ss = a.dq_stride[2];
+  p.dk_sb = a.dk_stride[0];
+  p.dk_sh = a.dk_stride[1];
+  p.dk_ss = a.dk_stride[2];
+  p.dv_sb = a.dv_stride[0];
+  p.dv_sh = a.dv_stride[1];
+  p.dv_ss = a.dv_stride[2];
+  p.l_sb = a.lse_stride[0];
+  p.l_sh = a.lse_stride[1];
+  p.l_ss = a.lse_stride[2];
+  p.B = a.batch;
+  p.Hq = a.heads_q;
+  p.Hkv = a.heads_kv;
+  p.Sq = a.seqlen_q;
+  p.Skv = a.seqlen_kv;
+  p.D = a.head_dim;
+  p.q_offset = a.q_offset;
+  p.causal = a.causal ? 1 : 0;
+  // a window of 2^30 or more masks nothing (positions are below 2^30); clamping it
+  // keeps every position - window + 1 inside int32
+  p.window = a.window > 0 ? min(a.window, 0x40000000) : 0;
+  p.ratio = a.heads_q / a.heads_kv;
+  p.sq_pad = static_cast<int>(sq_padded(a.seqlen_q));
+  p.n_qt = p.sq_pad / kQTile;
+  p.n_kt = (a.seqlen_kv + kDkvKeys - 1) / kDkvKeys;
+  const bool softcap = a.softcap > 0.0f;
+  if (softcap) {
+    p.score_mul = a.scale / a.softcap;
+    p.cap_mul = a.softcap * kLog2e;
+    p.tanh_mul = 2.0f * kLog2e * a.scale / a.softcap;
+  } else {
+    p.score_mul = a.scale * kLog2e;
+    p.cap_mul = 0.0f;
+    p.tanh_mul = 0.0f;
+  }
+  p.scale = a.scale;
+  float* ws = static_cast<float*>(a.workspace);
+  const int64_t rows = static_cast<int64_t>(a.batch) * a.heads_q * p.sq_pad;
+  p.lse2 = ws;
+  p.di = ws + rows;
+
+  const int64_t grid_pre = rows / 32;
+  const int64_t grid_dq = static_cast<int64_t>(p.n_qt) * a.batch * a.heads_q;
+  const int64_t grid_dkv = static_cast<int64_t>(p.n_kt) * a.batch * a.heads_kv;
+  if (grid_pre > 0x7fffffff || grid_dq > 0x7fffffff || grid_dkv > 0x7fffffff) {
+    return FFA_ERR_TOO_LARGE;
+  }
+  if (grid_pre == 0 || grid_dq == 0) return FFA_OK;
+  p.xcd_remap_dq = (grid_dq % 8 == 0) ? 1 : 0;
+  p.xcd_remap_dkv = (grid_dkv % 8 == 0) ? 1 : 0;
+  if (a.dtype == FFA_DTYPE_BF16) {
+    launch_tag<Bf16Tag>(p, softcap, static_cast<int>(grid_pre), static_cast<int>(grid_dkv),
+                        static_cast<int>(grid_dq), stream);
+  } else {
+    launch_tag<F16Tag>(p, softcap, static_cast<int>(grid_pre), static_cast<int>(grid_dkv),
+                       static_cast<int>(grid_dq), stream);
+  }
+  return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
+}
+
+}  // namespace ffa

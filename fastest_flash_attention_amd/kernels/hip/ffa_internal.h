@@ -25,6 +25,10 @@ size_t mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,
                                   int32_t max_context_len, int32_t tokens_per_split);
 int launch_mla_decode(const ffa_mla_decode_args& a, hipStream_t stream);
 
+// Attention backward: preprocess, dK/dV and dQ kernels.
+size_t attn_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q);
+int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream);
+
 // get_kv gather.
 int launch_paged_gather(const ffa_paged_gather_args& a, hipStream_t stream);
 int launch_paged_append(const ffa_paged_append_args& a, hipStream_t stream);

@@ -1,6 +1,7 @@
-"""Ops layer: the forward entry point, the autograd wrapper, block-sparse masks and
+"""Ops layer: the forward and backward entry points, the autograd wrapper, block-sparse masks and
 the KV caches."""
 
+from .attention_backward import fastest_flash_attn_backward
 from .attention_forward import fastest_flash_attn_forward
 from .attention_func import FastestFlashAttnFunc, fastest_flash_attn_func
 from .block_sparse import (
@@ -14,6 +15,7 @@ from .mla_decode import MLALatentCache, fastest_flash_mla_decode
 
 __all__ = [
     "fastest_flash_attn_forward",
+    "fastest_flash_attn_backward",
     "FastestFlashAttnFunc",
     "fastest_flash_attn_func",
     "ContinuousKVCache",

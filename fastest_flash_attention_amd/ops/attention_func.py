@@ -1,9 +1,11 @@
-"""Autograd wrapper around the HIP forward (reference ops/attention_func.py:20-125).
+"""Autograd wrapper around the HIP forward and backward (reference
+ops/attention_func.py:20-125).
 
-The forward is ``fastest_flash_attn_forward`` with ``return_lse=True`` (the reference
-saves q, k, v, O, LSE for a recompute backward). The backward pass is not part of
-this build: calling it raises NotImplementedError instead of silently routing through
-another implementation.
+The forward is ``fastest_flash_attn_forward`` with ``return_lse=True``; q, k, v, O and
+the LSE are saved (not the attention matrix) and the backward is
+``fastest_flash_attn_backward``, which recomputes P from them on the GPU. With
+``num_kv_heads`` (GQA) the saved K/V keep their own head count and the backward sums
+dK/dV over each head group.
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ from typing import Optional
 import torch
 from torch.autograd import Function
 
+from .attention_backward import fastest_flash_attn_backward
 from .attention_forward import fastest_flash_attn_forward
 
 
@@ -36,10 +39,13 @@ class FastestFlashAttnFunc(Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        raise NotImplementedError(
-            "fastest_flash_attention_amd implements the forward pass only; the attention "
-            "backward kernel is not part of this build"
+        q, k, v, output, lse = ctx.saved_tensors
+        dq, dk, dv = fastest_flash_attn_backward(
+            grad_output.contiguous(), q, k, v, output, lse,
+            scale=ctx.scale, causal=ctx.causal, block_size=ctx.block_size,
+            softcap=ctx.softcap, sliding_window=ctx.sliding_window,
         )
+        return dq, dk, dv, None, None, None, None, None, None, None
 
 
 def fastest_flash_attn_func(

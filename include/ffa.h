@@ -28,6 +28,13 @@
  *                              no MLA decode path; this one reads the compressed latent
  *                              cache instead of up-projected K/V.
  *   ffa_mla_decode_workspace_bytes: sizing helper of the MLA decode entry point.
+ *   ffa_attn_bwd           <- fastest_flash_attn_backward   ops/attention_backward.py:19-76
+ *                             (its GPU branch flash_attn_triton_backward
+ *                              kernels/triton_bwd.py:122-190; the CPU branch
+ *                              flash_attn_cpu_backward kernels/cpu_reference.py:319-427
+ *                              defines the semantics), reached from
+ *                             FastestFlashAttnFunc.backward ops/attention_func.py:61-90.
+ *   ffa_attn_bwd_workspace_bytes: sizing helper of the backward entry point.
  *   ffa_strerror, ffa_abi_version: error text / version probe, replacing the
  *                             availability probe check_triton_available utils.py:20-29.
  */
@@ -41,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FFA_ABI_VERSION 3
+#define FFA_ABI_VERSION 4
 
 typedef enum ffa_status {
   FFA_OK = 0,
@@ -51,7 +58,7 @@ typedef enum ffa_status {
   FFA_ERR_MISALIGNED = -4,       /* base not 16-byte aligned, or head_dim / a stride not a
                                     multiple of 8 elements (prefill) */
   FFA_ERR_GQA_RATIO = -5,        /* heads_q not a multiple of heads_kv */
-  FFA_ERR_WORKSPACE = -6,        /* decode workspace missing or too small */
+  FFA_ERR_WORKSPACE = -6,        /* workspace missing or too small */
   FFA_ERR_LAUNCH = -7,           /* hipGetLastError() reported a launch failure */
   FFA_ERR_NO_DEVICE = -8,        /* no usable HIP device / device query failed */
   FFA_ERR_TOO_LARGE = -9         /* a size exceeds what the kernels index with 32 bits */
@@ -280,6 +287,65 @@ typedef struct ffa_mla_decode_args {
 size_t ffa_mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,
                                       int32_t max_context_len, int32_t tokens_per_split);
 int ffa_mla_decode_fwd(const ffa_mla_decode_args* args, void* stream);
+
+/*
+ * Attention backward (recompute): gradients of the prefill forward above for one
+ * upstream gradient dO, from q, k, v, the forward's O and its natural-log LSE.
+ * Semantics (kernels/cpu_reference.py:319-427):
+ *   P   = exp(S - lse)  with S, the masks and softcap as in ffa_prefill_fwd
+ *         (a row with lse = -inf has P = 0)
+ *   D_i = sum_d dO[i, d] * O[i, d]                    fp32
+ *   dV  = P^T dO
+ *   dS  = P * (dO V^T - D_i), times 1 - tanh^2(q.k * scale / softcap) with softcap
+ *   dQ  = scale * dS K,   dK = scale * dS^T Q
+ * GQA: dK / dV of kv head j sum over the q heads j * ratio .. (j + 1) * ratio - 1.
+ * Layout: element strides [batch, head, seq, dim] (dim stride 1; dq/dk/dv written in
+ * place, no broadcast strides on them); lse strides [batch, head, seq]. All of dout,
+ * q, k, v, o, dq, dk, dv share the dtype (bf16 / fp16: fp32 accumulation, P and dS
+ * rounded to the dtype for the matrix products). head_dim is 1..128 and a multiple of
+ * 8; every tensor is 16-byte aligned with batch/head/seq strides multiples of 8
+ * elements (FFA_ERR_MISALIGNED) and seq strides below 2^24 elements. The workspace
+ * (16-byte aligned, ffa_attn_bwd_workspace_bytes()) holds per-row statistics; the
+ * call overwrites all of it. Three kernels, no atomics: results do not depend on
+ * scheduling.
+ */
+typedef struct ffa_attn_bwd_args {
+  const void* dout;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const float* lse;
+  void* dq;
+  void* dk;
+  void* dv;
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t do_stride[4];
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t o_stride[4];
+  int64_t dq_stride[4];
+  int64_t dk_stride[4];
+  int64_t dv_stride[4];
+  int64_t lse_stride[3];
+  int32_t batch;
+  int32_t heads_q;
+  int32_t heads_kv;
+  int32_t seqlen_q;
+  int32_t seqlen_kv;
+  int32_t head_dim;         /* 1..128 */
+  int32_t q_offset;
+  int32_t causal;
+  int32_t window;           /* <= 0: no sliding window */
+  float scale;              /* any finite value */
+  float softcap;            /* <= 0: no softcap */
+  int32_t dtype;            /* FFA_DTYPE_BF16 or FFA_DTYPE_FP16 */
+} ffa_attn_bwd_args;
+
+size_t ffa_attn_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q);
+int ffa_attn_bwd(const ffa_attn_bwd_args* args, void* stream);
 
 const char* ffa_strerror(int status);
 int ffa_abi_version(void);

@@ -1,0 +1,205 @@
+"""GPU parity of the attention backward (ffa_attn_bwd through fastest_flash_attn_backward
+and FastestFlashAttnFunc.backward) against the CPU oracle
+(oracle/reference_backward.py, itself pinned by fp64 autograd) on identical inputs:
+the same 16-bit q, k, v, dO and the same O (rounded to the input dtype) and LSE.
+
+Tolerance (the gradients have no tolerance of their own in the task statement; these
+bars are stated here, per tensor, relative to the oracle's magnitude): P and dS are
+rounded to the input's 16-bit type for the matrix products and the results are
+stored in it, so
+    max |got - ref| <= 2e-2 * max |ref|   and   mean |got - ref| <= 1e-2 * mean |ref|
+for bf16 (8-bit mantissa), a quarter of that for fp16 (11-bit).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fastest_flash_attention_amd as ffa
+from oracle import reference_backward as rb
+from oracle import reference_forward as rf
+from tests.gpu_util import np32, require_gpu, say, seeded
+
+pytestmark = pytest.mark.gpu
+
+BF16, F16 = torch.bfloat16, torch.float16
+
+
+def _oracle_forward(q, k, v, *, scale, causal, window, softcap, q_offset, two_pass=False):
+    """O (fp32) and LSE of the reference forward, K/V repeated to q's heads."""
+    ratio = q.shape[1] // k.shape[1]
+    kr, vr = np.repeat(np32(k), ratio, axis=1), np.repeat(np32(v), ratio, axis=1)
+    return rf.flash_attn_cpu_forward(np32(q), kr, vr, scale=scale, causal=causal,
+                                     softcap=softcap, sliding_window=window,
+                                     two_pass=two_pass, q_offset=q_offset, return_lse=True)
+
+
+def _check(got: torch.Tensor, ref: np.ndarray, dtype, what: str):
+    g = np32(got).astype(np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    assert g.shape == r.shape, (what, g.shape, r.shape)
+    assert np.isfinite(g).all(), f"{what}: non-finite gradient"
+    rel = 1.0 if dtype == BF16 else 0.25
+    err = np.abs(g - r)
+    if r.size == 0:
+        return
+    max_ref, mean_ref = float(np.abs(r).max()), float(np.abs(r).mean())
+    print(f"  {what}: max err {err.max():.3e} (ref max {max_ref:.3e}), "
+          f"mean err {err.mean():.3e} (ref mean {mean_ref:.3e})", flush=True)
+    assert err.max() <= 2e-2 * rel * max_ref + 1e-6, f"{what}: max err {err.max():.3e}"
+    assert err.mean() <= 1e-2 * rel * mean_ref + 1e-7, f"{what}: mean err {err.mean():.3e}"
+
+
+# (name, B, Hq, Hkv, Sq, Skv, D, q_offset, kwargs, dtype)
+CASES = [
+    ("plain", 2, 4, 4, 128, 128, 64, 0, {}, BF16),
+    ("causal_ragged", 1, 3, 3, 257, 257, 128, 0, {"causal": True}, BF16),
+    ("noncausal_ragged", 1, 2, 2, 200, 333, 128, 0, {}, BF16),
+    ("causal_window", 1, 2, 2, 300, 300, 128, 0, {"causal": True, "sliding_window": 37}, BF16),
+    ("window_noncausal", 1, 2, 2, 180, 180, 64, 0, {"sliding_window": 50}, BF16),
+    ("softcap_causal", 2, 2, 2, 150, 150, 64, 0, {"causal": True, "softcap": 10.0}, BF16),
+    ("gqa", 1, 8, 2, 256, 256, 128, 0, {"causal": True}, BF16),
+    ("mqa", 1, 4, 1, 96, 96, 64, 0, {}, BF16),
+    ("q_offset_causal", 1, 2, 2, 70, 300, 128, 230, {"causal": True}, BF16),
+    ("q_offset_window_softcap", 1, 4, 2, 45, 200, 64, 155,
+     {"causal": True, "sliding_window": 60, "softcap": 20.0}, BF16),
+    ("d40_padded", 1, 2, 2, 100, 100, 40, 0, {"causal": True}, BF16),
+    ("d96", 1, 2, 2, 77, 77, 96, 0, {"causal": True}, BF16),
+    ("d16", 2, 2, 2, 40, 40, 16, 0, {}, BF16),
+    ("fp16_softcap", 1, 4, 4, 200, 200, 128, 0, {"causal": True, "softcap": 30.0}, F16),
+    ("fp16_gqa_window", 2, 4, 2, 160, 160, 64, 0, {"causal": True, "sliding_window": 33}, F16),
+    ("single", 1, 2, 2, 1, 1, 64, 0, {}, BF16),
+    ("negative_scale", 1, 2, 2, 150, 150, 64, 0, {"causal": True, "scale": -0.2}, BF16),
+    ("zero_scale", 1, 2, 2, 70, 70, 64, 0, {"causal": True, "scale": 0.0}, BF16),
+    ("gqa_window_softcap", 2, 8, 2, 333, 333, 128, 0,
+     {"causal": True, "sliding_window": 100, "softcap": 50.0}, BF16),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_backward_parity(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, D, off, kw, dt = case
+    q = seeded((B, Hq, Sq, D), dt, 1)
+    k = seeded((B, Hkv, Skv, D), dt, 2)
+    v = seeded((B, Hkv, Skv, D), dt, 3)
+    do = seeded((B, Hq, Sq, D), dt, 4)
+    scale = kw.get("scale", 1.0 / math.sqrt(D))
+    causal = kw.get("causal", False)
+    window = kw.get("sliding_window")
+    softcap = kw.get("softcap")
+    o32, lse = _oracle_forward(q, k, v, scale=scale, causal=causal, window=window,
+                               softcap=softcap, q_offset=off)
+    o = torch.from_numpy(o32).to(dt)
+    say(f"backward {name} B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} off{off} {kw} {dt}")
+    dq, dk, dv = ffa.fastest_flash_attn_backward(
+        do.cuda(), q.cuda(), k.cuda(), v.cuda(), o.cuda(), torch.from_numpy(lse).cuda(),
+        scale=scale, causal=causal, softcap=softcap, sliding_window=window, q_offset=off)
+    torch.cuda.synchronize()
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    assert dq.dtype == dk.dtype == dv.dtype == dt
+    rq, rk, rv = rb.backward(np32(do), np32(q), np32(k), np32(v), np32(o), lse, scale=scale,
+                             causal=causal, softcap=softcap, sliding_window=window,
+                             q_offset=off)
+    _check(dq, rq, dt, f"{name} dq")
+    _check(dk, rk, dt, f"{name} dk")
+    _check(dv, rv, dt, f"{name} dv")
+
+
+def test_backward_deterministic():
+    """No atomics: two calls give bit-identical gradients."""
+    require_gpu()
+    B, H, S, D = 2, 4, 300, 128
+    q, k, v, do = (seeded((B, H, S, D), BF16, s).cuda() for s in (11, 12, 13, 14))
+    say("backward determinism")
+    o, lse = ffa.fastest_flash_attn_forward(q, k, v, causal=True, return_lse=True)
+    a = ffa.fastest_flash_attn_backward(do, q, k, v, o, lse, causal=True)
+    b = ffa.fastest_flash_attn_backward(do, q, k, v, o, lse, causal=True)
+    torch.cuda.synchronize()
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_autograd_func_matches_oracle():
+    """fastest_flash_attn_func forward + .backward() (the training entry point), 3D
+    inputs, against the oracle fed the HIP forward's own O and LSE."""
+    require_gpu()
+    B, S, D = 2, 190, 64
+    q, k, v = (seeded((B, S, D), BF16, s).cuda().requires_grad_() for s in (21, 22, 23))
+    do = seeded((B, S, D), BF16, 24).cuda()
+    say("autograd func 3D causal softcap")
+    out = ffa.fastest_flash_attn_func(q, k, v, causal=True, softcap=15.0)
+    out.backward(do)
+    torch.cuda.synchronize()
+    o, lse = ffa.fastest_flash_attn_forward(q.detach(), k.detach(), v.detach(), causal=True,
+                                            softcap=15.0, return_lse=True)
+    assert torch.equal(o, out.detach())
+    rq, rk, rv = rb.backward(np32(do)[:, None], np32(q)[:, None], np32(k)[:, None],
+                             np32(v)[:, None], np32(o)[:, None], np32(lse)[:, None],
+                             causal=True, softcap=15.0)
+    _check(q.grad, rq[:, 0], BF16, "func dq")
+    _check(k.grad, rk[:, 0], BF16, "func dk")
+    _check(v.grad, rv[:, 0], BF16, "func dv")
+
+
+def test_autograd_func_gqa_matches_oracle():
+    require_gpu()
+    B, Hq, Hkv, S, D = 1, 8, 2, 256, 128
+    q = seeded((B, Hq, S, D), BF16, 31).cuda().requires_grad_()
+    k = seeded((B, Hkv, S, D), BF16, 32).cuda().requires_grad_()
+    v = seeded((B, Hkv, S, D), BF16, 33).cuda().requires_grad_()
+    do = seeded((B, Hq, S, D), BF16, 34).cuda()
+    say("autograd func GQA")
+    out = ffa.fastest_flash_attn_func(q, k, v, causal=True, num_kv_heads=Hkv)
+    out.backward(do)
+    o, lse = ffa.fastest_flash_attn_forward(q.detach(), k.detach(), v.detach(), causal=True,
+                                            num_kv_heads=Hkv, return_lse=True)
+    rq, rk, rv = rb.backward(np32(do), np32(q), np32(k), np32(v), np32(o), np32(lse),
+                             causal=True)
+    _check(q.grad, rq, BF16, "gqa dq")
+    _check(k.grad, rk, BF16, "gqa dk")
+    _check(v.grad, rv, BF16, "gqa dv")
+
+
+def test_rows_without_keys_get_zero_gradient():
+    """A two-pass forward gives rows with no visible key lse = -inf; their P is 0 (the
+    reference's exp(-inf - (-inf)) would be NaN), so they add nothing to dK / dV and
+    get dq = 0. Here the window leaves rows 0..q_offset-window-… empty: q_offset < 0."""
+    require_gpu()
+    B, H, Sq, Skv, D = 1, 2, 64, 64, 64
+    q, k, v, do = (seeded((B, H, n, D), BF16, s) for n, s in ((Sq, 41), (Skv, 42), (Skv, 43),
+                                                               (Sq, 44)))
+    off = -20  # rows 0..19 sit before key 0: causal leaves them no key
+    o32, lse = _oracle_forward(q, k, v, scale=0.125, causal=True, window=None, softcap=None,
+                               q_offset=off, two_pass=True)
+    assert np.isneginf(lse[:, :, :20]).all() and np.isfinite(lse[:, :, 20:]).all()
+    o = torch.from_numpy(np.nan_to_num(o32)).to(BF16)
+    say("backward rows without keys")
+    dq, dk, dv = ffa.fastest_flash_attn_backward(
+        do.cuda(), q.cuda(), k.cuda(), v.cuda(), o.cuda(), torch.from_numpy(lse).cuda(),
+        scale=0.125, causal=True, q_offset=off)
+    torch.cuda.synchronize()
+    assert torch.all(dq[:, :, :20] == 0)
+    # the live rows alone give the oracle's dK / dV
+    live = slice(20, None)
+    rq, rk, rv = rb.backward(np32(do)[:, :, live], np32(q)[:, :, live], np32(k), np32(v),
+                             np32(o)[:, :, live], lse[:, :, live], scale=0.125, causal=True,
+                             q_offset=off + 20)
+    _check(dq[:, :, live], rq, BF16, "live dq")
+    _check(dk, rk, BF16, "live dk")
+    _check(dv, rv, BF16, "live dv")
+
+
+def test_backward_rejects_unsupported():
+    require_gpu()
+    x = torch.zeros(1, 2, 8, 192, dtype=BF16, device="cuda")
+    lse = torch.zeros(1, 2, 8, 1, device="cuda")
+    with pytest.raises(ValueError):
+        ffa.fastest_flash_attn_backward(x, x, x, x, x, lse)
+    y = torch.zeros(1, 2, 8, 64, device="cuda")
+    with pytest.raises(TypeError):
+        ffa.fastest_flash_attn_backward(y, y, y, y, y, lse)

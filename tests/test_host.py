@@ -151,6 +151,7 @@ def _c_layout(struct: str, fields: list[str]) -> dict:
     (_lib.PagedDecodeArgs, "ffa_paged_decode_args"),
     (_lib.PagedAppendArgs, "ffa_paged_append_args"),
     (_lib.MlaDecodeArgs, "ffa_mla_decode_args"),
+    (_lib.AttnBwdArgs, "ffa_attn_bwd_args"),
 ])
 def test_ctypes_struct_matches_header(cls, cname):
     fields = [f for f, _ in cls._fields_]
@@ -212,6 +213,27 @@ def test_validation_errors_without_device(lib):
     assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -4  # q not 16-byte aligned
     m.q, m.block_table_stride = 16, 3
     assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -1
+    bw = _lib.AttnBwdArgs()
+    assert lib.ffa_attn_bwd(None, None) == -1
+    bw.dtype, bw.head_dim, bw.batch, bw.heads_q, bw.heads_kv = 2, 64, 1, 4, 2
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -2  # no fp32 backward kernel
+    bw.dtype, bw.head_dim = 0, 192
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -3  # head_dim <= 128
+    bw.head_dim, bw.heads_q = 64, 3
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -5
+    bw.heads_q, bw.seqlen_q, bw.seqlen_kv = 4, 100, 100
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -1  # null pointers
+    bw.dout = bw.q = bw.k = bw.v = bw.o = bw.lse = bw.dq = bw.dk = bw.dv = 16
+    for name in ("do_stride", "q_stride", "k_stride", "v_stride", "o_stride", "dq_stride",
+                 "dk_stride", "dv_stride"):
+        getattr(bw, name)[:] = [4 * 100 * 64, 100 * 64, 64, 1]
+    bw.workspace, bw.workspace_bytes = 16, 8
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -6
+    bw.workspace_bytes = lib.ffa_attn_bwd_workspace_bytes(1, 4, 100)
+    bw.q_stride[2] = 68
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -4  # row stride not 8-aligned
+    bw.q_stride[2], bw.scale = 64, float("nan")
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -1
 
 
 def test_workspace_sizing(lib):
@@ -227,6 +249,9 @@ def test_workspace_sizing(lib):
     assert lib.ffa_mla_decode_workspace_bytes(2, 8, 256, 1000, 0) == 2 * 8 * 2 * 257 * 4
     assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 5000, 4096) == 5 * 513 * 4
     assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 100, 40) == 2 * 513 * 4  # 40 -> 64
+    # backward: lse2 and D_i, fp32, rows padded to 128 per (batch, q head)
+    assert lib.ffa_attn_bwd_workspace_bytes(2, 3, 100) == 2 * 2 * 3 * 128 * 4
+    assert lib.ffa_attn_bwd_workspace_bytes(1, 1, 256) == 2 * 256 * 4
 
 
 # ---------------------------------------------------------------------------------
