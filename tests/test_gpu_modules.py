@@ -65,14 +65,48 @@ def test_mla_module_d192():
     assert torch.isfinite(out).all()
 
 
-def test_training_mode_forward_and_backward_contract():
+def _mha_reference_fp32(m, x):
+    """The module's training forward restated in plain fp32 torch on the CPU (same bf16
+    weights and input, upcast): projections, causal softmax attention, output projection."""
+    W = {n: p.detach().float().cpu().requires_grad_() for n, p in m.named_parameters()}
+    xr = x.detach().float().cpu().requires_grad_()
+    B, S, Hd = xr.shape
+    H, D = m.num_heads, m.head_dim
+
+    def heads(t):
+        return t.view(B, S, H, D).transpose(1, 2)
+
+    q = heads(xr @ W["q_proj.weight"].t())
+    k = heads(xr @ W["k_proj.weight"].t())
+    v = heads(xr @ W["v_proj.weight"].t())
+    s = (q @ k.transpose(-1, -2)) * m.scale
+    mask = torch.triu(torch.ones(S, S, dtype=torch.bool), diagonal=1)
+    p = torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1)
+    a = (p @ v).transpose(1, 2).reshape(B, S, Hd)
+    return a @ W["o_proj.weight"].t(), xr, W
+
+
+def test_training_mode_forward_and_backward():
+    """Training mode routes through the autograd function: gradients reach the input and
+    every projection weight and match the fp32 CPU restatement of the module."""
     require_gpu()
     torch.manual_seed(3)
     m = ffa.FastestFlashMHA(hidden_size=128, num_heads=2, causal=True).cuda().to(torch.bfloat16)
     m.train()
     x = torch.randn(1, 40, 128, device="cuda", dtype=torch.bfloat16, requires_grad=True)
-    say("module training-mode forward")
+    g = torch.randn(1, 40, 128, dtype=torch.bfloat16)
+    say("module training-mode forward + backward")
     out = m(x)
     assert out.shape == (1, 40, 128)
-    with pytest.raises(NotImplementedError):
-        out.float().sum().backward()
+    out.backward(g.cuda())
+    ref, xr, W = _mha_reference_fp32(m, x)
+    ref.backward(g.float())
+    pairs = [(out, ref), (x.grad, xr.grad)]
+    pairs += [(p.grad, W[n].grad) for n, p in m.named_parameters()]
+    for got, want in pairs:
+        assert got is not None and want is not None
+        got = got.detach().float().cpu()
+        want = want.detach()
+        err = (got - want).abs()
+        assert err.max() <= 5e-2 * want.abs().max(), (err.max(), want.abs().max())
+        assert err.mean() <= 2e-2 * want.abs().mean(), (err.mean(), want.abs().mean())
