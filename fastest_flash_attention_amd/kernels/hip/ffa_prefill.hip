@@ -134,17 +134,21 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   // The loads are issued from inline asm (wave-uniform tile base + 32-bit lane offset):
   // the compiler neither holds a 64-bit address per load nor guards later LDS reads
   // with vmcnt waits; completion is the explicit wait_vmcnt0 before each tile barrier.
-  auto issue_tile = [&](const char* base, int64_t stride, const uint32_t (&off)[S::LPT],
-                        uint16_t* dst, int t) {
-    const int kt0 = t * BN;
-    const char* tb = base + static_cast<int64_t>(kt0) * stride * 2;
-    if (kt0 + BN <= Skv) {
+  // K and V tiles are issued in order, so each tensor keeps a running tile base that
+  // advances by one tile per issue (one 64-bit scalar add per tile).
+  const int64_t k_tile_bytes = static_cast<int64_t>(BN) * p.k_ss * 2;
+  const int64_t v_tile_bytes = static_cast<int64_t>(BN) * p.v_ss * 2;
+  const int t_full = Skv / BN;  // tiles below this index hold BN keys
+  auto issue_tile = [&](const char*& tb, int64_t tile_bytes, int64_t stride,
+                        const uint32_t (&off)[S::LPT], uint16_t* dst, int t) {
+    if (t < t_full) {
 #pragma unroll
       for (int j = 0; j < S::LPT; ++j) {
         load_lds16_async(tb, off[j], lds_addr(dst + (4 * j + wave) * 512));
       }
     } else {
       // last tile: rows past Skv re-read row Skv-1 (their scores are masked to -inf)
+      const int kt0 = t * BN;
 #pragma unroll
       for (int j = 0; j < S::LPT; ++j) {
         const int row = ((4 * j + wave) * 64 + lane) / S::CPR;
@@ -153,7 +157,10 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
         load_lds16_async(tb, off[j] - back, lds_addr(dst + (4 * j + wave) * 512));
       }
     }
+    tb += tile_bytes;
   };
+  const char* k_next = kbytes + static_cast<int64_t>(t_begin) * k_tile_bytes;
+  const char* v_next = vbytes + static_cast<int64_t>(t_begin) * v_tile_bytes;
 
   // ---- per-lane LDS operand addresses (element offsets inside one tile buffer) ----
   // K operand of k-step ks for 32-key block nb: row 32nb + l32, chunk 2ks + g.
@@ -309,9 +316,9 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   f32x16 s_cur[S::NB];
   f32x16 s_nxt[S::NB];
   if (nt > 0) {
-    issue_tile(kbytes, p.k_ss, k_off, k_lds[0], t_begin);
-    issue_tile(vbytes, p.v_ss, v_off, v_lds[0], t_begin);
-    if (nt > 1) issue_tile(kbytes, p.k_ss, k_off, k_lds[1], t_begin + 1);
+    issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, k_lds[0], t_begin);
+    issue_tile(v_next, v_tile_bytes, p.v_ss, v_off, v_lds[0], t_begin);
+    if (nt > 1) issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, k_lds[1], t_begin + 1);
     wait_vmcnt0();
     __syncthreads();
     if (wave_live) qk(k_lds[0], s_cur);
@@ -324,8 +331,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     const int t = t_begin + i;
     wait_vmcnt0();
     __syncthreads();
-    if (i + 2 < nt) issue_tile(kbytes, p.k_ss, k_off, k_lds[i & 1], t + 2);
-    if (i + 1 < nt) issue_tile(vbytes, p.v_ss, v_off, v_lds[(i + 1) & 1], t + 1);
+    if (i + 2 < nt) issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, k_lds[i & 1], t + 2);
+    if (i + 1 < nt) issue_tile(v_next, v_tile_bytes, p.v_ss, v_off, v_lds[(i + 1) & 1], t + 1);
     if (!wave_live) return;
     if (p.causal && t * BN > qwl_abs) return;  // past this wave's causal band
     if (i + 1 < nt) qk(k_lds[(i + 1) & 1], nxt);
