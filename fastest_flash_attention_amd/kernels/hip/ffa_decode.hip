@@ -6,7 +6,7 @@
 //
 // Decode (one query token per sequence, GQA group of G = Hq / Hkv query heads per KV
 // head) is split-K:
-//   split kernel  grid (splits, Hkv * column_groups, batch), 4 waves per workgroup.
+//   split kernel  grid (batch * Hkv * column_groups, splits), 4 waves per workgroup.
 //                 A workgroup streams tokens_per_split tokens of one (sequence, KV head)
 //                 straight from the pages; every K/V byte is read once and serves all
 //                 G query heads of the group (no repeat_kv). The block-table entries of
@@ -119,10 +119,16 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   __shared__ float red_l[kDecWaves][kCols];
   auto red_o = reinterpret_cast<float(*)[kCols][DP + 1]>(smem);
 
-  const int split = blockIdx.x;
-  const int hk = blockIdx.y / p.n_cg;
-  const int cg = blockIdx.y - hk * p.n_cg;
-  const int b = blockIdx.z;
+  // blockIdx.x = (sequence, KV head, column group), blockIdx.y = split: workgroups are
+  // dealt to the 8 XCDs round-robin by linear id, so every XCD gets whole KV heads of
+  // every sequence (with the split as the fast index, an XCD would get one split
+  // position of every sequence, and uneven lengths would load the XCDs unevenly).
+  const int split = blockIdx.y;
+  const int per_b = p.Hkv * p.n_cg;
+  const int b = blockIdx.x / per_b;
+  const int hkcg = blockIdx.x - b * per_b;
+  const int hk = hkcg / p.n_cg;
+  const int cg = hkcg - hk * p.n_cg;
   const int L = min(max(p.lens[b], 0), p.max_len);
   const int lo = p.window > 0 ? max(0, L - p.window) : 0;
   const int s_begin = max(split * p.tps, lo);
@@ -439,7 +445,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p
 //
 // Pool layout: [num_pages, page_size, DV + 64], token t of sequence b at page
 // block_tables[b][t / page_size], slot t % page_size (the PagedKVCache index law).
-// Workgroup = 4 waves for (split, 32-head group, sequence), two workgroups per CU.
+// Workgroup = 4 waves for (sequence, 32-head group) x split, two workgroups per CU.
 // 32-key tiles of the shared rows go HBM -> LDS (asm global_load_lds_dwordx4) into a
 // 2-stage ring. Wave w takes heads 16 * (w >> 1) + 0..15 (MFMA columns) and output dims
 // [(w & 1) DV/2, (w & 1 + 1) DV/2): it computes S^T = K Q^T for its 16 heads with
@@ -467,6 +473,7 @@ struct MlaParams {
   int bt_stride;
   int B, Hq, P, log2P, num_pages;
   int n_splits, tps, max_len;
+  int n_hg;  // 32-head groups
   float score_mul;  // scale * log2e
 };
 
@@ -499,9 +506,11 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   __shared__ __attribute__((aligned(1024))) uint16_t ring[kMlaStages][TILE];
   __shared__ int bt_lds[kMlaMaxSplit + 2];
 
-  const int split = blockIdx.x;
-  const int hg = blockIdx.y;
-  const int b = blockIdx.z;
+  // blockIdx.x = (sequence, head group), blockIdx.y = split (XCD balance, as in the
+  // paged decode kernel)
+  const int split = blockIdx.y;
+  const int b = blockIdx.x / p.n_hg;
+  const int hg = blockIdx.x - b * p.n_hg;
   const int L = min(max(p.lens[b], 0), p.max_len);
   const int s_begin = split * p.tps;
   const int s_end = min(s_begin + p.tps, L);
@@ -831,11 +840,12 @@ int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream) {
   p.ws_o = static_cast<float*>(a.workspace);
   p.ws_lse = p.ws_o + rows * p.dp;
 
-  const int64_t gy = static_cast<int64_t>(a.heads_kv) * p.n_cg;
-  if (gy > 65535 || a.batch > 65535 || static_cast<int64_t>(a.batch) * a.heads_q > 0x7fffffff) {
+  const int64_t gx = static_cast<int64_t>(a.batch) * a.heads_kv * p.n_cg;
+  if (gx > 0x7fffffff || p.n_splits > 65535 ||
+      static_cast<int64_t>(a.batch) * a.heads_q > 0x7fffffff) {
     return FFA_ERR_TOO_LARGE;
   }
-  const dim3 grid(p.n_splits, static_cast<unsigned>(gy), a.batch);
+  const dim3 grid(static_cast<unsigned>(gx), p.n_splits);
   if (a.dtype == FFA_DTYPE_BF16) {
     launch_decode_tag<Bf16Tag>(p, softcap, grid, stream);
   } else {
@@ -1000,11 +1010,13 @@ int launch_mla_decode(const ffa_mla_decode_args& a, hipStream_t stream) {
   cp.window = 0;
   cp.max_len = a.max_context_len;
 
-  const int64_t gy = (static_cast<int64_t>(a.heads_q) + 31) / 32;
-  if (gy > 65535 || a.batch > 65535 || static_cast<int64_t>(a.batch) * a.heads_q > 0x7fffffff) {
+  mp.n_hg = (a.heads_q + 31) / 32;
+  const int64_t gx = static_cast<int64_t>(a.batch) * mp.n_hg;
+  if (gx > 0x7fffffff || mp.n_splits > 65535 ||
+      static_cast<int64_t>(a.batch) * a.heads_q > 0x7fffffff) {
     return FFA_ERR_TOO_LARGE;
   }
-  const dim3 grid(mp.n_splits, static_cast<unsigned>(gy), a.batch);
+  const dim3 grid(static_cast<unsigned>(gx), mp.n_splits);
   if (a.dtype == FFA_DTYPE_BF16) {
     launch_mla_tag<Bf16Tag>(mp, cp, a.dim_v, grid, stream);
   } else {

@@ -201,7 +201,8 @@ int ffa_paged_append(const ffa_paged_append_args* args, void* stream);
  * context_lens[b] == 0 gives O = 0 and lse = -inf. head_dim % 8 == 0; q, the pools and
  * the workspace are 16-byte aligned and q's strides are multiples of 8
  * (FFA_ERR_MISALIGNED). tokens_per_split is rounded up to a multiple of 16 and clamped
- * to [32, 2048].
+ * to [32, 2048]; ceil(max_context_len / tokens_per_split) must not exceed 65535
+ * (FFA_ERR_TOO_LARGE).
  * Split-K: each sequence is cut into chunks of tokens_per_split tokens processed
  * by independent workgroups; partials (O, lse) go to the caller's workspace and
  * are merged by logsumexp weights.
@@ -257,7 +258,8 @@ int ffa_paged_decode_fwd(const ffa_paged_decode_args* args, void* stream);
  * dim_v is 256 or 512 and dim_rope is 64 (FFA_ERR_UNSUPPORTED_HEAD_DIM). q and
  * kv_pages are 16-byte aligned, q's strides multiples of 8 (FFA_ERR_MISALIGNED).
  * tokens_per_split (0: library default 512) is rounded up to a multiple of 32 and
- * capped at 1024; partials go to the workspace as in ffa_paged_decode_fwd.
+ * capped at 1024, and ceil(max_context_len / tokens_per_split) must not exceed 65535
+ * (FFA_ERR_TOO_LARGE); partials go to the workspace as in ffa_paged_decode_fwd.
  */
 typedef struct ffa_mla_decode_args {
   const void* q;

@@ -302,6 +302,8 @@ def test_paged_cache_out_of_pages_matches_reference_state():
 def test_auto_tokens_per_split():
     from fastest_flash_attention_amd.ops.kv_cache import _auto_tokens_per_split
 
-    assert _auto_tokens_per_split(64, 8, 32768) == 512   # long-context batch: 512-token splits
-    assert _auto_tokens_per_split(1, 8, 4096) == 64       # small batch: shortest split
-    assert _auto_tokens_per_split(4, 8, 8192) == 128      # 4*8*64 = 2048 workgroups
+    assert _auto_tokens_per_split(64, 8, 32768) == 2048  # long-context batch: longest split
+    assert _auto_tokens_per_split(2, 8, 32768) == 2048   # 2*8*16 = 256 workgroups
+    assert _auto_tokens_per_split(4, 8, 8192) == 1024    # 4*8*8 = 256 workgroups
+    assert _auto_tokens_per_split(1, 8, 4096) == 128     # 1*8*32 = 256 workgroups
+    assert _auto_tokens_per_split(1, 1, 100) == 64       # tiny problem: shortest split
