@@ -5,8 +5,9 @@ Headline workload: bf16 causal prefill, B=4, H=32, S=
 D=128, through the drop-in ``fastest_flash_attn_forward``. A step is one forward over
 that batch with q/k/v already resident in HBM. Second workload in the same line:
 paged GQA decode (BASELINE cfg4: B=64, 32 q heads / 8 kv heads, D=128, page 16,
-context lengths U[512, 32768], random page permutation), and a third: MLA decode over
-the compressed latent cache (BASELINE cfg5 decode: batch 32 at context 4096).
+context lengths U[512, 32768], random page permutation), a third: MLA decode over the
+compressed latent cache (BASELINE cfg5 decode: batch 32 at context 4096), and a fourth:
+the attention backward at the north-star shape.
 
 Algorithmic work: prefill FLOPs = 4 * B * H * D * N_valid, N_valid = exact number of
 unmasked (q, k) pairs; decode bytes = K/V bytes of exactly context_len tokens + q + o +
@@ -188,6 +189,46 @@ def bench_prefill(name: str, steps: int, warmup: int, cpu_budget: float):
     }
 
 
+def bench_backward(steps: int, warmup: int):
+    """Attention backward (fastest_flash_attn_backward: preprocess, dK/dV and dQ kernels)
+    at the north-star shape, from the forward's O and LSE. Algorithmic FLOPs =
+    10 * D per visible (q, k) pair (S, dP, dV, dQ, dK: five products); the kernels
+    execute 14 * D (S and dP are recomputed by the dQ kernel instead of accumulating dQ
+    with atomics)."""
+    import torch
+
+    import fastest_flash_attention_amd as ffa
+    from fastest_flash_attention_amd.ops.attention_backward import fastest_flash_attn_backward
+
+    cfg = PREFILL["north_star"]
+    B, H, S, D = cfg["B"], cfg["Hq"], cfg["S"], cfg["D"]
+    g = torch.Generator().manual_seed(0)
+    q, k, v, do = (torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).cuda()
+                   for _ in range(4))
+    o, lse = ffa.fastest_flash_attn_forward(q, k, v, causal=True, return_lse=True)
+
+    def step():
+        fastest_flash_attn_backward(do, q, k, v, o, lse, causal=True)
+
+    ms_event, ms_wall = time_steps(step, steps, warmup)
+    pairs = n_valid_pairs_fast(S, True, None)
+    flops = 10.0 * B * H * D * pairs
+    achieved = flops / (ms_event * 1e-3) / 1e12
+    return {
+        "metric": "attention backward TFLOP/s (10 * D per visible pair)",
+        "value": flops / (ms_wall * 1e-3) / 1e12,
+        "unit": "TFLOP/s",
+        "ms_per_step": ms_wall,
+        "kernel_ms": ms_event,
+        "flops": flops,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
+                     "traffic": profiled_traffic("bwd_dkdv_kernel_north_star.md")},
+        "config": {"workload": "north_star_backward", "batch": B, "heads": H, "seq_len": S,
+                   "head_dim": D, "causal": True},
+    }
+
+
 def bench_decode(steps: int, warmup: int):
     import torch
 
@@ -285,6 +326,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="north_star", choices=sorted(PREFILL))
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="time budget of the CPU baseline sample (0 disables it)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -315,6 +357,7 @@ def main() -> int:
     pre = bench_prefill(args.workload, args.steps, args.warmup, args.cpu_seconds)
     dec = None if args.no_decode else bench_decode(args.steps, args.warmup)
     mla = None if args.no_decode else bench_mla_decode(args.steps, args.warmup)
+    bwd = None if args.no_backward else bench_backward(args.steps, args.warmup)
     line = {
         "metric": "prefill attn TFLOP/s (% bf16 MFMA peak); paged-decode HBM GB/s (% peak)",
         "value": pre["value"],
@@ -333,6 +376,7 @@ def main() -> int:
         "cpu_baseline": pre["cpu_baseline"],
         "decode": dec,
         "mla_decode": mla,
+        "backward": bwd,
     }
     print(json.dumps(line), flush=True)
     return 0
