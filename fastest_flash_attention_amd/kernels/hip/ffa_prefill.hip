@@ -29,6 +29,8 @@
 // Grid order: heaviest causal query tiles first, and (when the grid is a multiple of
 // 8) consecutive tiles of one head are placed on one XCD so its K/V stay in that L2.
 
+#include <type_traits>
+
 #include "ffa_common.h"
 #include "ffa_internal.h"
 #include "ffa_prefill_common.h"
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   const int64_t v_tile_bytes = static_cast<int64_t>(BN) * p.v_ss * 2;
   const int t_full = Skv / BN;  // tiles below this index hold BN keys
   auto issue_tile = [&](const char*& tb, int64_t tile_bytes, int64_t stride,
-                        const uint32_t (&off)[S::LPT], uint16_t* dst, int t) {
+                        const uint32_t (&off)[S::LPT], uint16_t* dst, int t) __attribute__((always_inline)) {
     if (t < t_full) {
 #pragma unroll
       for (int j = 0; j < S::LPT; ++j) {
@@ -156,6 +158,15 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
         const uint32_t back = static_cast<uint32_t>(over * stride * 2);
         load_lds16_async(tb, off[j] - back, lds_addr(dst + (4 * j + wave) * 512));
       }
+    }
+    tb += tile_bytes;
+  };
+  // A tile known to hold BN keys (no tail handling, no test).
+  auto issue_full = [&](const char*& tb, int64_t tile_bytes, const uint32_t (&off)[S::LPT],
+                        uint16_t* dst) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < S::LPT; ++j) {
+      load_lds16_async(tb, off[j], lds_addr(dst + (4 * j + wave) * 512));
     }
     tb += tile_bytes;
   };
@@ -204,7 +215,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   float m_run = kNegInf;
   float l_run = 0.0f;
 
-  auto qk = [&](const uint16_t* kl, f32x16 (&sacc)[S::NB]) {
+  auto qk = [&](const uint16_t* kl, f32x16 (&sacc)[S::NB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
@@ -233,7 +244,10 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   };
 
   // Online softmax of tile t (scores in sacc) then O^T += V^T P^T from V tile vl.
-  auto softmax_pv = [&](f32x16 (&sacc)[S::NB], int t, const uint16_t* vl) {
+  // MAYMASK (std::true_type / std::false_type): whether this tile can need an element
+  // mask at all; the fast steps below only handle tiles that cannot.
+  auto softmax_pv = [&](f32x16 (&sacc)[S::NB], int t, const uint16_t* vl, auto maymask) __attribute__((always_inline)) {
+    constexpr bool MAYMASK = decltype(maymask)::value;
     const int kt0 = t * BN;
     if constexpr (SOFTCAP) {
 #pragma unroll
@@ -244,15 +258,15 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
         }
       }
     }
-    const bool need_mask = (kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
-                           (p.window > 0 && kt0 < qwl_abs - p.window + 1) ||
-                           kmask_row != nullptr;
+    const bool need_mask = MAYMASK && ((kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
+                                       (p.window > 0 && kt0 < qwl_abs - p.window + 1) ||
+                                       p.kmask != nullptr);
     if (need_mask) {
       // keys kt0 .. kt0 + BN - 1 of the block mask (BN divides 64, kt0 % BN == 0)
       // pre-shifted by this lane half's key offset 4g, so each element tests a bit at
       // a compile-time position (no per-element 64-bit shift constants to hold)
       const uint64_t kbits =
-          kmask_row != nullptr ? kmask_row[kt0 >> 6] >> ((kt0 & 63) + 4 * g) : ~uint64_t{0};
+          p.kmask != nullptr ? kmask_row[kt0 >> 6] >> ((kt0 & 63) + 4 * g) : ~uint64_t{0};
       const int key0 = kt0 + 4 * g;
 #pragma unroll
       for (int nb = 0; nb < S::NB; ++nb) {
@@ -327,7 +341,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   // LDS; it issues K(t+2) and V(t+1) into the buffers iteration i-1 finished reading,
   // computes S^T(t+1) (MFMA) ahead of softmax(t) (VALU), then P V(t). The loop body is
   // written twice so the two score buffers swap roles without copies.
-  auto step = [&](int i, f32x16 (&cur)[S::NB], f32x16 (&nxt)[S::NB]) {
+  auto step = [&](int i, f32x16 (&cur)[S::NB], f32x16 (&nxt)[S::NB]) __attribute__((always_inline)) {
     const int t = t_begin + i;
     wait_vmcnt0();
     __syncthreads();
@@ -336,9 +350,47 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     if (!wave_live) return;
     if (p.causal && t * BN > qwl_abs) return;  // past this wave's causal band
     if (i + 1 < nt) qk(k_lds[(i + 1) & 1], nxt);
-    softmax_pv(cur, t, v_lds[i & 1]);
+    softmax_pv(cur, t, v_lds[i & 1], std::true_type{});
   };
-  for (int i = 0; i < nt; i += 2) {
+  // The same iteration for a tile where every test above is known to pass: K(t+2) and
+  // V(t+1) exist and hold BN keys, the wave is live and the tile needs no element mask.
+  // The same barrier count and the same loads as `step`, without the tests.
+  auto fast_step = [&](int i, f32x16 (&cur)[S::NB], f32x16 (&nxt)[S::NB]) __attribute__((always_inline)) {
+    const int t = t_begin + i;
+    wait_vmcnt0();
+    __syncthreads();
+    issue_full(k_next, k_tile_bytes, k_off, k_lds[i & 1]);
+    issue_full(v_next, v_tile_bytes, v_off, v_lds[(i + 1) & 1]);
+    qk(k_lds[(i + 1) & 1], nxt);
+    softmax_pv(cur, t, v_lds[i & 1], std::false_type{});
+  };
+  // This wave's fast range [i_lo, i_hi) (wave-uniform): tiles t + 2 < nt and holding BN
+  // keys, right of the window's left edge for the wave's last row, and (causal) wholly
+  // at or left of the wave's first row. No block mask.
+  int i_lo = 0;
+  int i_hi = 0;
+  if (wave_live && p.kmask == nullptr) {
+    i_hi = min(nt - 2, t_full - t_begin - 2);
+    if (p.causal) i_hi = min(i_hi, (qw0_abs + 1) / BN - t_begin);
+    if (p.window > 0) {
+      const int edge = qwl_abs - p.window + 1;  // first key every row of the wave sees
+      i_lo = edge > 0 ? (edge + BN - 1) / BN - t_begin : 0;
+      i_lo = max(i_lo, 0);
+    }
+  }
+  // Three loops over tile pairs (the loop body is written twice so the two score
+  // buffers swap roles without copies): general pairs up to the fast range, fast pairs,
+  // general pairs to the end.
+  int i = 0;
+  for (; i < nt && !(i >= i_lo && i + 1 < i_hi); i += 2) {
+    step(i, s_cur, s_nxt);
+    if (i + 1 < nt) step(i + 1, s_nxt, s_cur);
+  }
+  for (; i + 1 < i_hi; i += 2) {
+    fast_step(i, s_cur, s_nxt);
+    fast_step(i + 1, s_nxt, s_cur);
+  }
+  for (; i < nt; i += 2) {
     step(i, s_cur, s_nxt);
     if (i + 1 < nt) step(i + 1, s_nxt, s_cur);
   }
@@ -515,10 +567,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillP
       for (int r = 0; r < 16; ++r) sacc[r] = p.cap_mul * tanh_approx(sacc[r] * p.score_mul);
     }
     const bool need_mask = (kt0 + kF32BN > Skv) || (p.causal && kt0 + kF32BN - 1 > qw0_abs) ||
-                           (p.window > 0 && kt0 < qwl_abs - p.window + 1) || kmask_row != nullptr;
+                           (p.window > 0 && kt0 < qwl_abs - p.window + 1) || p.kmask != nullptr;
     if (need_mask) {
       const uint64_t kbits =
-          kmask_row != nullptr ? kmask_row[kt0 >> 6] >> (kt0 & 63) : ~uint64_t{0};
+          p.kmask != nullptr ? kmask_row[kt0 >> 6] >> (kt0 & 63) : ~uint64_t{0};
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int off = 8 * (r >> 2) + 4 * g + (r & 3);
