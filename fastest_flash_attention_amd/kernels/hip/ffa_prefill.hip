@@ -161,12 +161,17 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     }
     tb += tile_bytes;
   };
-  // A tile known to hold BN keys (no tail handling, no test).
+  // LDS byte address of this wave's first load slot in buffer 0 of K and of V (uniform,
+  // SGPRs): load j of buffer b writes at base + b * TILE * 2 + j * 4 KiB.
+  const uint32_t k_wlds = __builtin_amdgcn_readfirstlane(lds_addr(&k_lds[0][0]) + wave * 1024);
+  const uint32_t v_wlds = __builtin_amdgcn_readfirstlane(lds_addr(&v_lds[0][0]) + wave * 1024);
+  // A tile known to hold BN keys (no tail handling, no test) into buffer B.
   auto issue_full = [&](const char*& tb, int64_t tile_bytes, const uint32_t (&off)[S::LPT],
-                        uint16_t* dst) __attribute__((always_inline)) {
+                        uint32_t wlds, auto buf) __attribute__((always_inline)) {
+    constexpr uint32_t B = decltype(buf)::value;
 #pragma unroll
     for (int j = 0; j < S::LPT; ++j) {
-      load_lds16_async(tb, off[j], lds_addr(dst + (4 * j + wave) * 512));
+      load_lds16_async(tb, off[j], wlds + B * S::TILE * 2 + j * 4096);
     }
     tb += tile_bytes;
   };
@@ -355,14 +360,16 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   // The same iteration for a tile where every test above is known to pass: K(t+2) and
   // V(t+1) exist and hold BN keys, the wave is live and the tile needs no element mask.
   // The same barrier count and the same loads as `step`, without the tests.
-  auto fast_step = [&](int i, f32x16 (&cur)[S::NB], f32x16 (&nxt)[S::NB]) __attribute__((always_inline)) {
+  // PAR = i & 1, known at compile time in the fast loop (it starts at an even i).
+  auto fast_step = [&](int i, f32x16 (&cur)[S::NB], f32x16 (&nxt)[S::NB], auto par) __attribute__((always_inline)) {
+    constexpr int PAR = decltype(par)::value;
     const int t = t_begin + i;
     wait_vmcnt0();
     __syncthreads();
-    issue_full(k_next, k_tile_bytes, k_off, k_lds[i & 1]);
-    issue_full(v_next, v_tile_bytes, v_off, v_lds[(i + 1) & 1]);
-    qk(k_lds[(i + 1) & 1], nxt);
-    softmax_pv(cur, t, v_lds[i & 1], std::false_type{});
+    issue_full(k_next, k_tile_bytes, k_off, k_wlds, std::integral_constant<uint32_t, PAR>{});
+    issue_full(v_next, v_tile_bytes, v_off, v_wlds, std::integral_constant<uint32_t, 1 - PAR>{});
+    qk(k_lds[1 - PAR], nxt);
+    softmax_pv(cur, t, v_lds[PAR], std::false_type{});
   };
   // This wave's fast range [i_lo, i_hi) (wave-uniform): tiles t + 2 < nt and holding BN
   // keys, right of the window's left edge for the wave's last row, and (causal) wholly
@@ -387,8 +394,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     if (i + 1 < nt) step(i + 1, s_nxt, s_cur);
   }
   for (; i + 1 < i_hi; i += 2) {
-    fast_step(i, s_cur, s_nxt);
-    fast_step(i + 1, s_nxt, s_cur);
+    fast_step(i, s_cur, s_nxt, std::integral_constant<int, 0>{});
+    fast_step(i + 1, s_nxt, s_cur, std::integral_constant<int, 1>{});
   }
   for (; i < nt; i += 2) {
     step(i, s_cur, s_nxt);
