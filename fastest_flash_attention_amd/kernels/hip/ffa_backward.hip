@@ -305,18 +305,33 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
     q_off[j] = static_cast<uint32_t>(row * p.q_ss * 2 + cq * 16);
     do_off[j] = static_cast<uint32_t>(row * p.do_ss * 2 + cq * 16);
   }
-  auto issue = [&](int it, int buf) {
-    const int hq = hk * p.ratio + it / ntq;
-    const int q0 = (qt_begin + it % ntq) * kDkvRows;
-    const char* qb = reinterpret_cast<const char*>(p.q + b * p.q_sb + hq * p.q_sh +
-                                                   static_cast<int64_t>(q0) * p.q_ss);
-    const char* db = reinterpret_cast<const char*>(p.dout + b * p.do_sb + hq * p.do_sh +
-                                                   static_cast<int64_t>(q0) * p.do_ss);
+  // Tiles are visited q head by q head of the group, q tiles ascending within each.
+  // The next tile to issue is tracked incrementally (head r of the group, tile index
+  // qi, running byte pointers) instead of dividing the iteration index.
+  int is_r = 0;
+  int is_qi = 0;
+  const char* is_qb = nullptr;
+  const char* is_db = nullptr;
+  int64_t is_ws = 0;
+  const int64_t q_tile_bytes = static_cast<int64_t>(kDkvRows) * p.q_ss * 2;
+  const int64_t do_tile_bytes = static_cast<int64_t>(kDkvRows) * p.do_ss * 2;
+  auto is_head = [&]() {
+    const int hq = hk * p.ratio + is_r;
+    const int q0 = qt_begin * kDkvRows;
+    is_qb = reinterpret_cast<const char*>(p.q + b * p.q_sb + hq * p.q_sh +
+                                          static_cast<int64_t>(q0) * p.q_ss);
+    is_db = reinterpret_cast<const char*>(p.dout + b * p.do_sb + hq * p.do_sh +
+                                          static_cast<int64_t>(q0) * p.do_ss);
+    is_ws = (static_cast<int64_t>(b) * p.Hq + hq) * p.sq_pad + q0;
+  };
+  is_head();
+  auto issue = [&](int buf) {
+    const int q0 = (qt_begin + is_qi) * kDkvRows;
     if (q0 + kDkvRows <= Sq) {
 #pragma unroll
       for (int j = 0; j < LPT; ++j) {
-        load_lds16_async(qb, q_off[j], lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
-        load_lds16_async(db, do_off[j], lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(is_qb, q_off[j], lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(is_db, do_off[j], lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
       }
     } else {
       // rows past Sq re-read row Sq - 1: their lse2 is +inf, so P = dS = 0
@@ -326,16 +341,24 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
         const int over = max(0, q0 + row - (Sq - 1));
         const uint32_t qback = static_cast<uint32_t>(over * p.q_ss * 2);
         const uint32_t dback = static_cast<uint32_t>(over * p.do_ss * 2);
-        load_lds16_async(qb, q_off[j] - qback, lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
-        load_lds16_async(db, do_off[j] - dback, lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(is_qb, q_off[j] - qback, lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
+        load_lds16_async(is_db, do_off[j] - dback, lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
       }
     }
     if (wave == 0) {
       // lanes 0-7: lse2 rows q0 .. q0+31, lanes 8-15: D_i; the other lanes repeat them
       // into the unused rest of the 1 KiB stats buffer
-      const int64_t ws = (static_cast<int64_t>(b) * p.Hq + hq) * p.sq_pad + q0 + 4 * (lane & 7);
-      const float* src = ((lane & 8) ? p.di : p.lse2) + ws;
+      const float* src = ((lane & 8) ? p.di : p.lse2) + is_ws + 4 * (lane & 7);
       load_lds16_async(src, lds_addr(&st_lds[buf][0]));
+    }
+    if (++is_qi == ntq) {
+      is_qi = 0;
+      ++is_r;
+      if (is_r < p.ratio) is_head();
+    } else {
+      is_qb += q_tile_bytes;
+      is_db += do_tile_bytes;
+      is_ws += kDkvRows;
     }
   };
 
@@ -353,13 +376,15 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
     }
   }
 
-  if (nit > 0) issue(0, 0);
+  if (nit > 0) issue(0);
+  int cur_qi = 0;  // q tile index (within [0, ntq)) of iteration it
   for (int it = 0; it < nit; ++it) {
     const int buf = it & 1;
     wait_vmcnt0();
     __syncthreads();
-    if (it + 1 < nit) issue(it + 1, buf ^ 1);
-    const int q0 = (qt_begin + it % ntq) * kDkvRows;
+    if (it + 1 < nit) issue(buf ^ 1);
+    const int q0 = (qt_begin + cur_qi) * kDkvRows;
+    if (++cur_qi == ntq) cur_qi = 0;
     const int q0_abs = p.q_offset + q0;
     if (!wave_live) continue;
     if (p.causal && kw0 > q0_abs + kDkvRows - 1) continue;
@@ -377,13 +402,26 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
       sacc[r] = 0.0f;
       dpacc[r] = 0.0f;
     }
+    // operands one k-step ahead of the MFMAs that consume them
+    u32x4 aq = *reinterpret_cast<const u32x4*>(ql + row_rd(a_rd, 0));
+    u32x4 ad = *reinterpret_cast<const u32x4*>(dl + row_rd(a_rd, 0));
+    u32x4 bv = *reinterpret_cast<const u32x4*>(vw + row_rd(a_rd, 0));
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
-      const u32x4 aq = *reinterpret_cast<const u32x4*>(ql + row_rd(a_rd, ks));
-      const u32x4 ad = *reinterpret_cast<const u32x4*>(dl + row_rd(a_rd, ks));
-      const u32x4 bv = *reinterpret_cast<const u32x4*>(vw + row_rd(a_rd, ks));
+      u32x4 aq_n, ad_n, bv_n;
+      if (ks + 1 < S::KS) {
+        aq_n = *reinterpret_cast<const u32x4*>(ql + row_rd(a_rd, ks + 1));
+        ad_n = *reinterpret_cast<const u32x4*>(dl + row_rd(a_rd, ks + 1));
+        bv_n = *reinterpret_cast<const u32x4*>(vw + row_rd(a_rd, ks + 1));
+      }
+      __builtin_amdgcn_sched_barrier(0);
       sacc = E::mfma32(aq, kreg[ks], sacc);
       dpacc = E::mfma32(ad, bv, dpacc);
+      if (ks + 1 < S::KS) {
+        aq = aq_n;
+        ad = ad_n;
+        bv = bv_n;
+      }
     }
 
     // element (row 8i + 4g + j, key l32) sits in accumulator 4i + j
