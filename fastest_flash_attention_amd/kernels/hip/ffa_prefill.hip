@@ -42,6 +42,10 @@ using namespace pf;
 
 constexpr int kThreads = 256;
 constexpr int kBlockM = 128;
+// With a block mask, a workgroup first lists the KV tiles that hold any visible key for
+// its rows and visits only those; sweeps longer than this many tiles visit every tile.
+constexpr int kMaxLiveTiles = 2048;
+constexpr int kTileFull = 0x8000;  // list entry flag: the block mask keeps the whole tile
 template <int DP, int BN>
 struct Shape {
   static constexpr int CPR = DP / 8;            // 16-byte chunks per row
@@ -65,6 +69,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   using E = Elem<Tag>;
   __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][S::TILE];
   __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][S::TILE];
+  __shared__ uint16_t live_lds[kMaxLiveTiles];  // block mask: the tiles to visit
+  __shared__ int live_cnt[4];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -109,6 +115,53 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   const uint64_t* kmask_row =
       p.kmask != nullptr ? p.kmask + static_cast<int64_t>(min(qrow, p.Sq - 1) / p.ref_bq) * p.kmask_words
                          : nullptr;
+
+  // Block mask: list the tiles of [t_begin, t_begin + nt) whose keys have any set bit
+  // in the key mask of the workgroup's rows (rows q0 .. q_last, i.e. reference row
+  // blocks rb0 .. rb1). A tile without one contributes nothing (every score is masked),
+  // so skipping it changes no result; the fully-masked-row LSE comes from the
+  // reference's visited-tile counts, not from the tiles this kernel visits.
+  const bool use_list = p.kmask != nullptr && nt <= kMaxLiveTiles;
+  int n_it = nt;  // iterations of the sweep: nt, or the live tiles with a block mask
+  if (use_list) {
+    const int rb0 = q0 / p.ref_bq;
+    const int rb1 = q_last / p.ref_bq;
+    int n_live = 0;
+    for (int base = 0; base < nt; base += kThreads) {
+      const int i = base + tid;
+      bool live = false;
+      bool full = true;  // every key of the tile set for every row: no element mask
+      if (i < nt) {
+        const int kt0 = (t_begin + i) * BN;
+        const uint64_t all = BN < 64 ? (uint64_t{1} << (BN & 63)) - 1 : ~uint64_t{0};
+        for (int rb = rb0; rb <= rb1; ++rb) {
+          uint64_t w = p.kmask[static_cast<int64_t>(rb) * p.kmask_words + (kt0 >> 6)];
+          if constexpr (BN < 64) w = (w >> (kt0 & 63)) & all;
+          live = live || w != 0;
+          full = full && w == all;
+        }
+      }
+      const uint64_t bal = __ballot(live);
+      if (lane == 0) live_cnt[wave] = __popcll(bal);
+      __syncthreads();
+      int off = n_live;
+      for (int w = 0; w < wave; ++w) off += live_cnt[w];
+      if (live) {
+        live_lds[off + __popcll(bal & ((uint64_t{1} << lane) - 1))] =
+            static_cast<uint16_t>(i | (full ? kTileFull : 0));
+      }
+      n_live += live_cnt[0] + live_cnt[1] + live_cnt[2] + live_cnt[3];
+      __syncthreads();
+    }
+    n_it = n_live;
+  }
+  auto tile_at = [&](int i) {
+    return t_begin + (use_list ? static_cast<int>(live_lds[i] & (kTileFull - 1)) : i);
+  };
+  // whether the block mask needs element tests on sweep position i
+  auto kmask_partial = [&](int i) {
+    return p.kmask != nullptr && !(use_list && (live_lds[i] & kTileFull));
+  };
 
   // Scores stay in raw units until the exponent: p = exp2(s*c - m*c), with s = q.k and
   // c = scale*log2e, or with softcap s = tanh(q.k * scale / cap) and c = cap*log2e.
@@ -177,6 +230,16 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   };
   const char* k_next = kbytes + static_cast<int64_t>(t_begin) * k_tile_bytes;
   const char* v_next = vbytes + static_cast<int64_t>(t_begin) * v_tile_bytes;
+  // Issue K (V) tile t: in tile order the running pointer is already there; a live-tile
+  // list can jump, so there the pointer is set from t first.
+  auto issue_k = [&](int t, uint16_t* dst) __attribute__((always_inline)) {
+    if (use_list) k_next = kbytes + static_cast<int64_t>(t) * k_tile_bytes;
+    issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, dst, t);
+  };
+  auto issue_v = [&](int t, uint16_t* dst) __attribute__((always_inline)) {
+    if (use_list) v_next = vbytes + static_cast<int64_t>(t) * v_tile_bytes;
+    issue_tile(v_next, v_tile_bytes, p.v_ss, v_off, dst, t);
+  };
 
   // ---- per-lane LDS operand addresses (element offsets inside one tile buffer) ----
   // K operand of k-step ks for 32-key block nb: row 32nb + l32, chunk 2ks + g.
@@ -251,7 +314,8 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   // Online softmax of tile t (scores in sacc) then O^T += V^T P^T from V tile vl.
   // MAYMASK (std::true_type / std::false_type): whether this tile can need an element
   // mask at all; the fast steps below only handle tiles that cannot.
-  auto softmax_pv = [&](f32x16 (&sacc)[S::NB], int t, const uint16_t* vl, auto maymask) __attribute__((always_inline)) {
+  auto softmax_pv = [&](f32x16 (&sacc)[S::NB], int t, const uint16_t* vl, auto maymask,
+                        bool kpartial) __attribute__((always_inline)) {
     constexpr bool MAYMASK = decltype(maymask)::value;
     const int kt0 = t * BN;
     if constexpr (SOFTCAP) {
@@ -265,7 +329,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     }
     const bool need_mask = MAYMASK && ((kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
                                        (p.window > 0 && kt0 < qwl_abs - p.window + 1) ||
-                                       p.kmask != nullptr);
+                                       kpartial);
     if (need_mask) {
       // keys kt0 .. kt0 + BN - 1 of the block mask (BN divides 64, kt0 % BN == 0)
       // pre-shifted by this lane half's key offset 4g, so each element tests a bit at
@@ -334,10 +398,10 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
 
   f32x16 s_cur[S::NB];
   f32x16 s_nxt[S::NB];
-  if (nt > 0) {
-    issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, k_lds[0], t_begin);
-    issue_tile(v_next, v_tile_bytes, p.v_ss, v_off, v_lds[0], t_begin);
-    if (nt > 1) issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, k_lds[1], t_begin + 1);
+  if (n_it > 0) {
+    issue_k(tile_at(0), k_lds[0]);
+    issue_v(tile_at(0), v_lds[0]);
+    if (n_it > 1) issue_k(tile_at(1), k_lds[1]);
     wait_vmcnt0();
     __syncthreads();
     if (wave_live) qk(k_lds[0], s_cur);
@@ -347,15 +411,15 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   // computes S^T(t+1) (MFMA) ahead of softmax(t) (VALU), then P V(t). The loop body is
   // written twice so the two score buffers swap roles without copies.
   auto step = [&](int i, f32x16 (&cur)[S::NB], f32x16 (&nxt)[S::NB]) __attribute__((always_inline)) {
-    const int t = t_begin + i;
+    const int t = tile_at(i);
     wait_vmcnt0();
     __syncthreads();
-    if (i + 2 < nt) issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, k_lds[i & 1], t + 2);
-    if (i + 1 < nt) issue_tile(v_next, v_tile_bytes, p.v_ss, v_off, v_lds[(i + 1) & 1], t + 1);
+    if (i + 2 < n_it) issue_k(tile_at(i + 2), k_lds[i & 1]);
+    if (i + 1 < n_it) issue_v(tile_at(i + 1), v_lds[(i + 1) & 1]);
     if (!wave_live) return;
     if (p.causal && t * BN > qwl_abs) return;  // past this wave's causal band
-    if (i + 1 < nt) qk(k_lds[(i + 1) & 1], nxt);
-    softmax_pv(cur, t, v_lds[i & 1], std::true_type{});
+    if (i + 1 < n_it) qk(k_lds[(i + 1) & 1], nxt);
+    softmax_pv(cur, t, v_lds[i & 1], std::true_type{}, kmask_partial(i));
   };
   // The same iteration for a tile where every test above is known to pass: K(t+2) and
   // V(t+1) exist and hold BN keys, the wave is live and the tile needs no element mask.
@@ -369,7 +433,7 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
     issue_full(k_next, k_tile_bytes, k_off, k_wlds, std::integral_constant<uint32_t, PAR>{});
     issue_full(v_next, v_tile_bytes, v_off, v_wlds, std::integral_constant<uint32_t, 1 - PAR>{});
     qk(k_lds[1 - PAR], nxt);
-    softmax_pv(cur, t, v_lds[PAR], std::false_type{});
+    softmax_pv(cur, t, v_lds[PAR], std::false_type{}, false);
   };
   // This wave's fast range [i_lo, i_hi) (wave-uniform): tiles t + 2 < nt and holding BN
   // keys, right of the window's left edge for the wave's last row, and (causal) wholly
@@ -389,17 +453,17 @@ __global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const
   // buffers swap roles without copies): general pairs up to the fast range, fast pairs,
   // general pairs to the end.
   int i = 0;
-  for (; i < nt && !(i >= i_lo && i + 1 < i_hi); i += 2) {
+  for (; i < n_it && !(i >= i_lo && i + 1 < i_hi); i += 2) {
     step(i, s_cur, s_nxt);
-    if (i + 1 < nt) step(i + 1, s_nxt, s_cur);
+    if (i + 1 < n_it) step(i + 1, s_nxt, s_cur);
   }
   for (; i + 1 < i_hi; i += 2) {
     fast_step(i, s_cur, s_nxt, std::integral_constant<int, 0>{});
     fast_step(i + 1, s_nxt, s_cur, std::integral_constant<int, 1>{});
   }
-  for (; i < nt; i += 2) {
+  for (; i < n_it; i += 2) {
     step(i, s_cur, s_nxt);
-    if (i + 1 < nt) step(i + 1, s_nxt, s_cur);
+    if (i + 1 < n_it) step(i + 1, s_nxt, s_cur);
   }
 
   const float l_tot = wave_pair_sum(l_run);

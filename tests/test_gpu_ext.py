@@ -54,6 +54,56 @@ def test_block_mask_parity(case):
         assert np.all(np32(o)[:, :, :bs] == 0)
 
 
+# Masks that leave whole 64-key tiles of a workgroup's rows empty, so the kernel's
+# live-tile list skips them: (name, Sq, Skv, D, block, mask kind, kwargs)
+SKIP_CASES = [
+    ("local_b64", 1024, 1024, 128, 64, "local", {"causal": True}),
+    ("local_b128_noncausal", 768, 1024, 64, 128, "local", {}),
+    ("local_b32_d192_window", 640, 640, 192, 32, "local", {"causal": True, "sliding_window": 300}),
+    ("stripes_b64", 512, 1024, 128, 64, "stripes", {}),
+]
+
+
+@pytest.mark.parametrize("case", SKIP_CASES, ids=[c[0] for c in SKIP_CASES])
+def test_block_mask_tile_skipping_parity(case):
+    """Sparse block masks whose masked tiles the kernel never loads or computes: same O
+    and LSE as the reference loop, which skips them too (cpu_reference.py:220-222)."""
+    require_gpu()
+    name, Sq, Skv, D, bs, kind, kw = case
+    q = seeded((1, 2, Sq, D), BF16, 41)
+    k = seeded((1, 2, Skv, D), BF16, 42)
+    v = seeded((1, 2, Skv, D), BF16, 43)
+    n_br, n_bc = math.ceil(Sq / bs), math.ceil(Skv / bs)
+    if kind == "local":
+        bm = ffa.create_local_block_mask(Sq, Skv, bs, bs, local_radius=2 * bs).cpu()
+    else:
+        bm = torch.zeros(n_br, n_bc, dtype=torch.bool)
+        bm[:, ::3] = True   # every third key block
+    say(f"block_mask skip {name} Sq{Sq} Skv{Skv} D{D} bs{bs} {kind} {kw}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), block_size=bs,
+                                            block_mask=bm, return_lse=True, **kw)
+    torch.cuda.synchronize()
+    ro, rl = rf.forward(np32(q), np32(k), np32(v), block_size=bs, block_mask=bm.numpy(),
+                        return_lse=True, **kw)
+    assert_parity(o, ro, lse, rl, name)
+
+
+def test_block_mask_long_sweep_visits_every_tile():
+    """A sweep longer than the live-tile list (2048 tiles of 64 keys) visits every tile;
+    an all-true mask there still equals the unmasked result bit for bit."""
+    require_gpu()
+    Skv = 2048 * 64 + 1000
+    q = seeded((1, 1, 48, 64), BF16, 51).cuda()
+    k = seeded((1, 1, Skv, 64), BF16, 52).cuda()
+    v = seeded((1, 1, Skv, 64), BF16, 53).cuda()
+    say(f"block_mask long sweep Skv{Skv}")
+    dense, dl = ffa.fastest_flash_attn_forward(q, k, v, block_size=64, return_lse=True)
+    full = torch.ones(1, math.ceil(Skv / 64), dtype=torch.bool)
+    masked, ml = ffa.fastest_flash_attn_forward(q, k, v, block_size=64, block_mask=full,
+                                                return_lse=True)
+    assert torch.equal(dense, masked) and torch.equal(dl, ml)
+
+
 def test_block_mask_all_ones_equals_dense():
     """The reference's own check (tests/test_fastest_flash.py:240-258): an all-True
     mask gives the unmasked result."""
