@@ -60,11 +60,14 @@ struct Shape {
 
 // Two workgroups per CU (2 waves per SIMD, <= 256 VGPRs) up to head_dim 192; the
 // 256-dim variant keeps 128 fp32 accumulators per lane and runs one wave per SIMD.
-template <int DP>
-constexpr int kMinBlocks = DP <= 192 ? 2 : 1;
+// head_dim 64 without softcap fits 168 VGPRs without spills: three workgroups per CU
+// (+4 % at S = 8192 on MI355X; with softcap that bound spills). head_dim 32 needs
+// fewer than 168 VGPRs anyway.
+template <int DP, bool SOFTCAP>
+constexpr int kMinBlocks = (DP == 64 && !SOFTCAP) ? 3 : (DP <= 192 ? 2 : 1);
 
 template <typename Tag, int DP, int BN, bool SOFTCAP>
-__global__ __launch_bounds__(kThreads, kMinBlocks<DP>) void prefill_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_kernel(const PrefillParams p) {
   using S = Shape<DP, BN>;
   using E = Elem<Tag>;
   __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][S::TILE];
