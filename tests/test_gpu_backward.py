@@ -165,6 +165,27 @@ def test_autograd_func_gqa_matches_oracle():
     _check(v.grad, rv, BF16, "gqa dv")
 
 
+def test_empty_inputs():
+    """No keys: dq = 0 and empty dk/dv; no queries or no batch: empty gradients."""
+    require_gpu()
+    from fastest_flash_attention_amd.ops.attention_backward import fastest_flash_attn_backward
+    q = seeded((1, 2, 6, 64), BF16, 71).cuda()
+    none = torch.zeros(1, 2, 0, 64, dtype=BF16, device="cuda")
+    say("backward empty: S_kv = 0")
+    o, lse = ffa.fastest_flash_attn_forward(q, none, none, return_lse=True)
+    dq, dk, dv = fastest_flash_attn_backward(seeded((1, 2, 6, 64), BF16, 72).cuda(), q, none,
+                                             none, o, lse)
+    assert dq.shape == q.shape and not dq.abs().any()
+    assert dk.shape == none.shape and dv.shape == none.shape
+    say("backward empty: S_q = 0, B = 0")
+    for shape in ((1, 2, 0, 64), (0, 2, 5, 64)):
+        z = torch.zeros(*shape, dtype=BF16, device="cuda")
+        lz = torch.zeros(*shape[:3], 1, dtype=torch.float32, device="cuda")
+        kv = z if shape[0] == 0 else seeded((1, 2, 5, 64), BF16, 73).cuda()
+        dq, dk, dv = fastest_flash_attn_backward(z, z, kv, kv, z, lz)
+        assert dq.shape == z.shape and dk.shape == kv.shape and not dk.abs().any()
+
+
 def test_rows_without_keys_get_zero_gradient():
     """A two-pass forward gives rows with no visible key lse = -inf; their P is 0 (the
     reference's exp(-inf - (-inf)) would be NaN), so they add nothing to dK / dV and

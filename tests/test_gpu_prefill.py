@@ -152,6 +152,27 @@ def test_special_values():
     assert np.abs(np32(o) - np32(kv).mean(axis=2, keepdims=True)).max() < 1e-2
 
 
+def test_empty_inputs():
+    """Degenerate shapes as the reference loop leaves them: no keys -> O = 0 and
+    LSE = -inf (no tile visited); no queries or no batch -> empty outputs."""
+    require_gpu()
+    q = seeded((1, 2, 5, 64), BF16, 61).cuda()
+    none = torch.zeros(1, 2, 0, 64, dtype=BF16, device="cuda")
+    say("empty: S_kv = 0")
+    o, lse = ffa.fastest_flash_attn_forward(q, none, none, return_lse=True)
+    ro, rl = rf.forward(np32(q), np32(none), np32(none), return_lse=True)
+    assert o.shape == ro.shape and not o.abs().any()
+    assert torch.isneginf(lse).all() and np.isneginf(rl).all()
+    say("empty: S_q = 0")
+    kv = seeded((1, 2, 7, 64), BF16, 62).cuda()
+    o, lse = ffa.fastest_flash_attn_forward(q[:, :, :0], kv, kv, causal=True, return_lse=True)
+    assert o.shape == (1, 2, 0, 64) and lse.shape == (1, 2, 0, 1)
+    say("empty: B = 0")
+    z = torch.zeros(0, 2, 9, 64, dtype=BF16, device="cuda")
+    o, lse = ffa.fastest_flash_attn_forward(z, z, z, causal=True, return_lse=True)
+    assert o.shape == z.shape and lse.shape == (0, 2, 9, 1)
+
+
 def test_rejects_unsupported():
     require_gpu()
     q = torch.randn(1, 1, 8, 16, device="cuda")
