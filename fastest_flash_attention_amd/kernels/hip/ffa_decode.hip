@@ -451,7 +451,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p
 // [(w & 1) DV/2, (w & 1 + 1) DV/2): it computes S^T = K Q^T for its 16 heads with
 // v_mfma_f32_16x16x32 (the 2 waves of a head group duplicate this small product rather
 // than exchanging P), fp32 softmax with exp2 and deferred rescale, and O^T += V^T P^T
-// with v_mfma_f32_16x16x16 on its DV/2 dims (V^T by ds_read_b64_tr_b16).
+// with one v_mfma_f32_16x16x32 per 16 dims of its DV/2 (V^T by ds_read_b64_tr_b16).
 // Normalised (O, lse) partials per split are merged by decode_combine_kernel.
 // ---------------------------------------------------------------------------------
 constexpr int kMlaWaves = 4;
@@ -644,14 +644,15 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
       }
       pk[kb] = u32x2{E::pack2(e[0], e[1]), E::pack2(e[2], e[3])};
     }
+    // One 32-deep MFMA per dim block: k-slots 8 g4 + 0..3 hold keys 4 g4 + 0..3 and
+    // slots 8 g4 + 4..7 keys 16 + 4 g4 + 0..3, in both operands.
+    const u32x4 pb = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
 #pragma unroll
     for (int db = 0; db < DBW; ++db) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int off = v_rd[db & 3] + (db >> 2) * 64 + kb * 16 * DQK;
-        const u32x2 a = lds_read_tr16(tl + off);  // dim 16 db + c16 of keys 4 g4 + 0..3
-        oacc[db] = E::mfma16k16(a, pk[kb], oacc[db]);
-      }
+      const int off = v_rd[db & 3] + (db >> 2) * 64;
+      const u32x2 a0 = lds_read_tr16(tl + off);  // dim 16 db + c16 of keys 4 g4 + 0..3
+      const u32x2 a1 = lds_read_tr16(tl + off + 16 * DQK);  // keys 16 + 4 g4 + 0..3
+      oacc[db] = E::mfma16(u32x4{a0[0], a0[1], a1[0], a1[1]}, pb, oacc[db]);
     }
   };
 
