@@ -328,8 +328,8 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   // three-workgroup head_dim 64 variant (168 VGPRs).
   constexpr bool IL = DP <= 128 && kMinBlocks<DP, SOFTCAP> <= 2;
   auto softmax_pv = [&](f32x16 (&sacc)[S::NB], int t, const uint16_t* vl, auto maymask,
-                        bool kpartial, f32x16 (&nxt)[S::NB], const uint16_t* kl, bool do_qk)
-      __attribute__((always_inline)) {
+                        bool kpartial, f32x16 (&nxt)[S::NB], const uint16_t* kl, bool do_qk,
+                        auto chunk_hook) __attribute__((always_inline)) {
     constexpr bool MAYMASK = decltype(maymask)::value;
     const int kt0 = t * BN;
     constexpr int KPC = (S::KS + S::NC - 1) / S::NC;
@@ -406,6 +406,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     for (int cc = 0; cc < S::NC; ++cc) {
       const int nb = cc >> 1;
       const int base = (cc & 1) * 8;
+      chunk_hook(cc);
       // V^T operands of the chunk first: their LDS latency overlaps the exp work
       u32x4 av[S::DB];
 #pragma unroll
@@ -463,7 +464,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     if (p.causal && t * BN > qwl_abs) return;  // past this wave's causal band
     if (!IL && i + 1 < n_it) qk(k_lds[(i + 1) & 1], nxt);
     softmax_pv(cur, t, v_lds[i & 1], std::true_type{}, kmask_partial(i), nxt, k_lds[(i + 1) & 1],
-               i + 1 < n_it);
+               i + 1 < n_it, [](int) {});
   };
   // The same iteration for a tile where every test above is known to pass: K(t+2) and
   // V(t+1) exist and hold BN keys, the wave is live and the tile needs no element mask.
@@ -474,10 +475,27 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     const int t = t_begin + i;
     wait_vmcnt0();
     __syncthreads();
-    issue_full(k_next, k_tile_bytes, k_off, k_wlds, std::integral_constant<uint32_t, PAR>{});
-    issue_full(v_next, v_tile_bytes, v_off, v_wlds, std::integral_constant<uint32_t, 1 - PAR>{});
-    if (!IL) qk(k_lds[1 - PAR], nxt);
-    softmax_pv(cur, t, v_lds[PAR], std::false_type{}, false, nxt, k_lds[1 - PAR], true);
+    if (!IL) {
+      issue_full(k_next, k_tile_bytes, k_off, k_wlds, std::integral_constant<uint32_t, PAR>{});
+      issue_full(v_next, v_tile_bytes, v_off, v_wlds, std::integral_constant<uint32_t, 1 - PAR>{});
+      qk(k_lds[1 - PAR], nxt);
+      softmax_pv(cur, t, v_lds[PAR], std::false_type{}, false, nxt, k_lds[1 - PAR], true, [](int) {});
+    } else {
+      // The tile loads spread over the P V chunks (chunk cc issues loads
+      // LPT cc / NC .. LPT (cc + 1) / NC - 1 of K(t+2) and of V(t+1)) rather than all
+      // right after the barrier, where the four waves' 32 KiB of requests at once stall
+      // their issue: +2-4 % on MI355X.
+      softmax_pv(cur, t, v_lds[PAR], std::false_type{}, false, nxt, k_lds[1 - PAR], true,
+                 [&](int cc) __attribute__((always_inline)) {
+#pragma unroll
+                   for (int j = S::LPT * cc / S::NC; j < S::LPT * (cc + 1) / S::NC; ++j) {
+                     load_lds16_async(k_next, k_off[j], k_wlds + PAR * S::TILE * 2 + j * 4096);
+                     load_lds16_async(v_next, v_off[j], v_wlds + (1 - PAR) * S::TILE * 2 + j * 4096);
+                   }
+                 });
+      k_next += k_tile_bytes;
+      v_next += v_tile_bytes;
+    }
   };
   // This wave's fast range [i_lo, i_hi) (wave-uniform): tiles t + 2 < nt and holding BN
   // keys, right of the window's left edge for the wave's last row, and (causal) wholly
