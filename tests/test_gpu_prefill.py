@@ -152,6 +152,31 @@ def test_special_values():
     assert np.abs(np32(o) - np32(kv).mean(axis=2, keepdims=True)).max() < 1e-2
 
 
+def test_constant_v_and_large_softcap():
+    """Closed forms: rows of V all equal -> O = that row for any q and mask (P is a
+    convex combination; its bf16 rounding moves O by < 2^-8 relative). A softcap far
+    above every score (1000 against |s| < 10) leaves the result within tolerance of no
+    softcap (c tanh(s/c) - s ~ s^3 / 3c^2)."""
+    require_gpu()
+    q = seeded((1, 2, 200, 128), BF16, 71)
+    k = seeded((1, 2, 200, 128), BF16, 72)
+    row = seeded((1, 2, 1, 128), BF16, 73)
+    v = row.expand(1, 2, 200, 128).contiguous()
+    for causal, window in ((False, None), (True, None), (True, 64)):
+        say(f"constant V causal={causal} window={window}")
+        o, _ = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), causal=causal,
+                                              sliding_window=window)
+        assert np.abs(np32(o) - np32(v)).max() <= 1e-2 * np.abs(np32(row)).max()
+    v2 = seeded((1, 2, 200, 128), BF16, 74)
+    say("softcap 1000 vs none")
+    o1, l1 = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v2.cuda(), causal=True,
+                                            softcap=1000.0, return_lse=True)
+    o0, l0 = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v2.cuda(), causal=True,
+                                            return_lse=True)
+    assert np.abs(np32(o1) - np32(o0)).max() < 2e-2
+    assert np.abs(np32(l1) - np32(l0)).max() < 1e-3
+
+
 def test_empty_inputs():
     """Degenerate shapes as the reference loop leaves them: no keys -> O = 0 and
     LSE = -inf (no tile visited); no queries or no batch -> empty outputs."""
