@@ -47,6 +47,36 @@ constexpr int kBlockM = 128;
 // its rows and visits only those; sweeps longer than this many tiles visit every tile.
 constexpr int kMaxLiveTiles = 2048;
 constexpr int kTileFull = 0x8000;  // list entry flag: the block mask keeps the whole tile
+// Workgroup -> (batch x head, query tile j; j = 0 is the heaviest causal tile). The
+// hardware deals linear workgroup ids round-robin to the 8 XCDs. With xcd_group = G,
+// XCD x owns heads [x HX, (x + 1) HX) (HX = B Hq / 8) and runs them G at a time, tiles
+// heaviest first and the G heads interleaved: K/V of a head stay in one XCD's L2 (the
+// G heads' tiles of one weight are resident together), and each group ends on its
+// lightest tiles instead of the last head's heaviest tiles starting near the end.
+// G = 1 is head after head. For causal launches the host picks G so that a group is
+// about 256 workgroups (4 per slot of the XCD's 32 CUs x 2): on MI355X +2-3 % with a
+// window (S = 8192), +6-10 % at S = 4096, within run-to-run noise at the S = 8192
+// north-star shape. Otherwise xcd_remap places consecutive ids on one XCD (G = 1).
+__device__ inline void work_item(const PrefillParams& p, int bid, int& bh, int& jq) {
+  if (p.xcd_group > 0) {
+    const int g = p.xcd_group;
+    const int hx = static_cast<int>(gridDim.x / p.n_qt) >> 3;
+    const int x = bid & 7;
+    const int k = bid >> 3;
+    const int gi = k / (g * p.n_qt);
+    const int r = k - gi * g * p.n_qt;
+    jq = r / g;
+    bh = x * hx + gi * g + (r - jq * g);
+    return;
+  }
+  if (p.xcd_remap) {
+    const int per_xcd = gridDim.x >> 3;
+    bid = (bid & 7) * per_xcd + (bid >> 3);
+  }
+  bh = bid / p.n_qt;
+  jq = bid - bh * p.n_qt;
+}
+
 template <int DP, int BN>
 struct Shape {
   static constexpr int CPR = DP / 8;            // 16-byte chunks per row
@@ -82,13 +112,10 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  int bid = blockIdx.x;
-  if (p.xcd_remap) {
-    const int per_xcd = gridDim.x >> 3;
-    bid = (bid & 7) * per_xcd + (bid >> 3);
-  }
-  const int bh = bid / p.n_qt;
-  const int jq = bid - bh * p.n_qt;
+  int bh, jq;
+  work_item(p, blockIdx.x, bh, jq);
+  bh = __builtin_amdgcn_readfirstlane(bh);  // uniform: keeps the tile bases in SGPRs
+  jq = __builtin_amdgcn_readfirstlane(jq);
   const int qt = p.causal ? (p.n_qt - 1 - jq) : jq;
   const int b = bh / p.Hq;
   const int h = bh - b * p.Hq;
@@ -609,13 +636,10 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillP
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  int bid = blockIdx.x;
-  if (p.xcd_remap) {
-    const int per_xcd = gridDim.x >> 3;
-    bid = (bid & 7) * per_xcd + (bid >> 3);
-  }
-  const int bh = bid / p.n_qt;
-  const int jq = bid - bh * p.n_qt;
+  int bh, jq;
+  work_item(p, blockIdx.x, bh, jq);
+  bh = __builtin_amdgcn_readfirstlane(bh);  // uniform: keeps the tile bases in SGPRs
+  jq = __builtin_amdgcn_readfirstlane(jq);
   const int qt = p.causal ? (p.n_qt - 1 - jq) : jq;
   const int b = bh / p.Hq;
   const int h = bh - b * p.Hq;
@@ -850,6 +874,14 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   if (grid64 > 0x7fffffff) return FFA_ERR_TOO_LARGE;
   const int grid = static_cast<int>(grid64);
   p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  p.xcd_group = 0;
+  const int64_t nbh = static_cast<int64_t>(a.batch) * a.heads_q;
+  if (p.causal && nbh % 8 == 0) {  // non-causal tiles weigh the same: no tail to avoid
+    const int64_t hx = nbh / 8;
+    int g = 1;
+    while (2 * g * static_cast<int64_t>(p.n_qt) <= 256 && hx % (2 * g) == 0) g *= 2;
+    p.xcd_group = g;
+  }
 
   if (a.dtype == FFA_DTYPE_BF16) {
     launch_tag<Bf16Tag>(p, softcap, grid, stream);
