@@ -53,10 +53,11 @@ constexpr int kTileFull = 0x8000;  // list entry flag: the block mask keeps the 
 // heaviest first and the G heads interleaved: K/V of a head stay in one XCD's L2 (the
 // G heads' tiles of one weight are resident together), and each group ends on its
 // lightest tiles instead of the last head's heaviest tiles starting near the end.
-// G = 1 is head after head. For causal launches the host picks G so that a group is
-// about 256 workgroups (4 per slot of the XCD's 32 CUs x 2): on MI355X +2-3 % with a
-// window (S = 8192), +6-10 % at S = 4096, within run-to-run noise at the S = 8192
-// north-star shape. Otherwise xcd_remap places consecutive ids on one XCD (G = 1).
+// G = 1 is head after head. For causal launches the host uses G = 2 (when a group stays
+// within 256 workgroups, 4 per slot of the XCD's 32 CUs x 2): +2-3 % at S = 8192 on
+// MI355X for +45 % HBM reads (1.00 -> 1.46 GB at the north-star shape); G = 4 gained
+// up to 4 % more on smaller shapes but read 2.86 GB (four heads' K/V overflow the
+// XCD's 4 MB L2). Otherwise xcd_remap places consecutive ids on one XCD (G = 1).
 __device__ inline void work_item(const PrefillParams& p, int bid, int& bh, int& jq) {
   if (p.xcd_group > 0) {
     const int g = p.xcd_group;
@@ -879,7 +880,7 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   if (p.causal && nbh % 8 == 0) {  // non-causal tiles weigh the same: no tail to avoid
     const int64_t hx = nbh / 8;
     int g = 1;
-    while (2 * g * static_cast<int64_t>(p.n_qt) <= 256 && hx % (2 * g) == 0) g *= 2;
+    while (g < 2 && 2 * g * static_cast<int64_t>(p.n_qt) <= 256 && hx % (2 * g) == 0) g *= 2;
     p.xcd_group = g;
   }
 
