@@ -79,7 +79,42 @@ struct BwdParams {
   float tanh_mul;  // 2*log2e*scale/softcap: tanh(x) = 1 - 2 / (1 + exp2(q.k * tanh_mul))
   float scale;
   int xcd_remap_dq, xcd_remap_dkv;
+  int xcd_group_dq, xcd_group_dkv;  // > 0: units per interleaved group on one XCD
 };
+
+// Workgroup -> (unit u = batch x head, tile j; j = 0 the heaviest causal tile) for a
+// grid of n_units x n_t workgroups dealt round-robin to the 8 XCDs. With group g > 0,
+// XCD x owns units [x HX, (x + 1) HX) (HX = n_units / 8) and runs them g at a time, the
+// g units' tiles interleaved heaviest first (each unit's K/V or Q/dO stay in one L2,
+// and each group ends on light tiles); otherwise, with remap, consecutive ids share an
+// XCD (unit after unit). The same order as the forward kernel's grid.
+__device__ inline void bwd_work_item(int bid, int n_t, int g, int remap, int& u, int& j) {
+  if (g > 0) {
+    const int hx = static_cast<int>(gridDim.x / n_t) >> 3;
+    const int x = bid & 7;
+    const int k = bid >> 3;
+    const int gi = k / (g * n_t);
+    const int r = k - gi * g * n_t;
+    j = r / g;
+    u = x * hx + gi * g + (r - j * g);
+  } else {
+    if (remap) {
+      const int per_xcd = gridDim.x >> 3;
+      bid = (bid & 7) * per_xcd + (bid >> 3);
+    }
+    u = bid / n_t;
+    j = bid - u * n_t;
+  }
+  u = __builtin_amdgcn_readfirstlane(u);
+  j = __builtin_amdgcn_readfirstlane(j);
+}
+
+// Group size for a causal grid of n_units x n_t (see bwd_work_item): two units when the
+// units split evenly over the 8 XCDs in pairs and a group stays within 256 workgroups.
+int bwd_xcd_group(int causal, int64_t n_units, int n_t) {
+  if (!causal || n_units % 16 != 0 || 2 * static_cast<int64_t>(n_t) > 256) return 0;
+  return 2;
+}
 
 // XOR swizzle of the 16-byte chunk index of tile row r. Row-wise MFMA operand reads
 // (16 lanes, 16 rows, one chunk each) need r -> swz(r) injective over 16 rows (within
@@ -240,13 +275,8 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  int bid = blockIdx.x;
-  if (p.xcd_remap_dkv) {
-    const int per_xcd = gridDim.x >> 3;
-    bid = (bid & 7) * per_xcd + (bid >> 3);
-  }
-  const int bh = bid / p.n_kt;
-  const int kt = bid - bh * p.n_kt;  // causal: low key tiles are seen by the most rows
+  int bh, kt;  // causal: low key tiles are seen by the most rows (heaviest first)
+  bwd_work_item(blockIdx.x, p.n_kt, p.xcd_group_dkv, p.xcd_remap_dkv, bh, kt);
   const int b = bh / p.Hkv;
   const int hk = bh - b * p.Hkv;
   const int D = p.D;
@@ -501,13 +531,8 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(const BwdParams p) 
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  int bid = blockIdx.x;
-  if (p.xcd_remap_dq) {
-    const int per_xcd = gridDim.x >> 3;
-    bid = (bid & 7) * per_xcd + (bid >> 3);
-  }
-  const int bh = bid / p.n_qt;
-  const int jq = bid - bh * p.n_qt;
+  int bh, jq;
+  bwd_work_item(blockIdx.x, p.n_qt, p.xcd_group_dq, p.xcd_remap_dq, bh, jq);
   const int qt = p.causal ? (p.n_qt - 1 - jq) : jq;
   const int b = bh / p.Hq;
   const int h = bh - b * p.Hq;
@@ -789,6 +814,8 @@ int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream) {
   if (grid_pre == 0 || grid_dq == 0) return FFA_OK;
   p.xcd_remap_dq = (grid_dq % 8 == 0) ? 1 : 0;
   p.xcd_remap_dkv = (grid_dkv % 8 == 0) ? 1 : 0;
+  p.xcd_group_dq = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_q, p.n_qt);
+  p.xcd_group_dkv = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_kv, p.n_kt);
   if (a.dtype == FFA_DTYPE_BF16) {
     launch_tag<Bf16Tag>(p, softcap, static_cast<int>(grid_pre), static_cast<int>(grid_dkv),
                         static_cast<int>(grid_dq), stream);
