@@ -323,7 +323,9 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=10)
+    # 50 untimed steps (~0.1 s of prefill work at the north-star shape): the MI355X clock
+    # needs that long under load to settle, and a cold start reads ~5 % low.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="north_star", choices=sorted(PREFILL))
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-backward", action="store_true")
