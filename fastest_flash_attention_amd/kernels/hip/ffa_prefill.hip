@@ -49,25 +49,30 @@ constexpr int kMaxLiveTiles = 2048;
 constexpr int kTileFull = 0x8000;  // list entry flag: the block mask keeps the whole tile
 // Workgroup -> (batch x head, query tile j; j = 0 is the heaviest causal tile). The
 // hardware deals linear workgroup ids round-robin to the 8 XCDs. With xcd_group = G,
-// XCD x owns heads [x HX, (x + 1) HX) (HX = B Hq / 8) and runs them G at a time, tiles
-// heaviest first and the G heads interleaved: K/V of a head stay in one XCD's L2 (the
-// G heads' tiles of one weight are resident together), and each group ends on its
-// lightest tiles instead of the last head's heaviest tiles starting near the end.
-// G = 1 is head after head. For causal launches the host uses G = 2 (when a group stays
-// within 256 workgroups, 4 per slot of the XCD's 32 CUs x 2): +2-3 % at S = 8192 on
-// MI355X for +45 % HBM reads (1.00 -> 1.46 GB at the north-star shape); G = 4 gained
-// up to 4 % more on smaller shapes but read 2.86 GB (four heads' K/V overflow the
-// XCD's 4 MB L2). Otherwise xcd_remap places consecutive ids on one XCD (G = 1).
+// XCD x owns heads [x HX, (x + 1) HX) (HX = B Hq / 8) and runs them head after head,
+// heaviest tile first, so each head's K/V stay in one L2 while its tiles run; only its
+// last G heads run interleaved (tile j of each in turn), so the launch ends on light
+// tiles instead of the last head's heaviest tiles starting near the end. Causal
+// launches use G = 2: on MI355X +2-3 % at S = 8192 and +4-8 % at S = 4096 over plain
+// head after head, for 1.26 GB of HBM reads per north-star launch against 1.00 (all
+// heads in interleaved pairs: same speed, 1.51 GB; in fours: 2.86 GB). Without
+// xcd_group, xcd_remap places consecutive ids on one XCD.
 __device__ inline void work_item(const PrefillParams& p, int bid, int& bh, int& jq) {
   if (p.xcd_group > 0) {
-    const int g = p.xcd_group;
     const int hx = static_cast<int>(gridDim.x / p.n_qt) >> 3;
     const int x = bid & 7;
     const int k = bid >> 3;
-    const int gi = k / (g * p.n_qt);
-    const int r = k - gi * g * p.n_qt;
-    jq = r / g;
-    bh = x * hx + gi * g + (r - jq * g);
+    const int gl = min(hx, p.xcd_group);
+    const int k0 = (hx - gl) * p.n_qt;  // tiles of the heads run one after another
+    if (k < k0) {
+      const int u = k / p.n_qt;
+      bh = x * hx + u;
+      jq = k - u * p.n_qt;
+    } else {
+      const int r = k - k0;
+      jq = r / gl;
+      bh = x * hx + (hx - gl) + (r - jq * gl);
+    }
     return;
   }
   if (p.xcd_remap) {
@@ -875,14 +880,9 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   if (grid64 > 0x7fffffff) return FFA_ERR_TOO_LARGE;
   const int grid = static_cast<int>(grid64);
   p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  p.xcd_group = 0;
+  // non-causal tiles weigh the same: no tail to avoid
   const int64_t nbh = static_cast<int64_t>(a.batch) * a.heads_q;
-  if (p.causal && nbh % 8 == 0) {  // non-causal tiles weigh the same: no tail to avoid
-    const int64_t hx = nbh / 8;
-    int g = 1;
-    while (g < 2 && 2 * g * static_cast<int64_t>(p.n_qt) <= 256 && hx % (2 * g) == 0) g *= 2;
-    p.xcd_group = g;
-  }
+  p.xcd_group = (p.causal && nbh % 8 == 0) ? 2 : 0;
 
   if (a.dtype == FFA_DTYPE_BF16) {
     launch_tag<Bf16Tag>(p, softcap, grid, stream);

@@ -29,7 +29,7 @@ struct PrefillParams {
   int ref_bq, ref_bkv;
   int masked_lse_mode;
   int xcd_remap;
-  int xcd_group;  // > 0: heads per interleaved group on one XCD (see prefill_kernel)
+  int xcd_group;  // > 0: how many last heads of each XCD run interleaved (work_item)
   const uint64_t* kmask;  // block mask expanded to keys, [n_br][kmask_words], or null
   int kmask_words;
   const int32_t* visited;  // reference tiles visited per row block (with kmask)
