@@ -361,17 +361,21 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   }
 }
 
-// One wave per (sequence, query head): O = sum_s w_s O_s / sum_s w_s with
-// w_s = exp(lse_s - max lse). Lane l owns dims 2l, 2l + 1 of each 128-dim slice, so a
+// One workgroup per (sequence, query head): O = sum_s w_s O_s / sum_s w_s with
+// w_s = exp(lse_s - max lse). Lane l owns dims 2l, 2l + 1 of a 128-dim slice, so a
 // split's partial row is one coalesced 512-byte read; splits are walked 8 at a time
-// to keep eight reads in flight per lane.
+// to keep eight reads in flight per lane. Wave w of the workgroup (blockDim.x / 64
+// waves) takes slices w, w + waves, ...: wide rows (the 512 MLA latent dims) are
+// launched with one wave per slice, so all slices' reads are in flight at once.
 template <typename Tag>
-__global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams p) {
   using E = Elem<Tag>;
   const int bh = blockIdx.x;
   const int b = bh / p.Hq;
   const int hq = bh - b * p.Hq;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n_waves = blockDim.x >> 6;
   const int L = min(max(p.lens[b], 0), p.max_len);
   const int lo = p.window > 0 ? max(0, L - p.window) : 0;
   const int s0 = lo / p.tps;
@@ -394,7 +398,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p
 
   uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh;
   const bool o_pair_aligned = (reinterpret_cast<uintptr_t>(orow) & 3u) == 0;
-  for (int d0 = 2 * lane; d0 < p.D; d0 += 128) {
+  for (int d0 = 2 * lane + 128 * wave; d0 < p.D; d0 += 128 * n_waves) {
     f32x2 acc = {0.0f, 0.0f};
     if (mm != kNegInf) {
       const float* col = p.ws_o + base * p.dp + d0;
@@ -428,7 +432,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(const DecodeParams p
       if (d0 + 1 < p.D) orow[d0 + 1] = static_cast<uint16_t>(pr >> 16);
     }
   }
-  if (lane == 0 && p.lse != nullptr) {
+  if (threadIdx.x == 0 && p.lse != nullptr) {
     p.lse[b * p.l_sb + hq * p.l_sh] = (mm != kNegInf && wsum > 0.0f) ? mm + logf(wsum) : kNegInf;
   }
 }
@@ -964,7 +968,8 @@ void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3
   } else {
     hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256>), grid, dim3(kMlaThreads), 0, s, mp);
   }
-  hipLaunchKernelGGL((decode_combine_kernel<Tag>), dim3(cp.B * cp.Hq), dim3(64), 0, s, cp);
+  // one wave per 128-dim slice of the dim_v = 256 or 512 latent output dims
+  hipLaunchKernelGGL((decode_combine_kernel<Tag>), dim3(cp.B * cp.Hq), dim3(dim_v / 2), 0, s, cp);
 }
 
 }  // namespace
