@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime before libffa.so)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libffa.so")
 
-FFA_ABI_VERSION = 4
+FFA_ABI_VERSION = 5
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
 FFA_DTYPE_FP32 = 2

@@ -6,12 +6,19 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
+
 #include "ffa.h"
 #include "ffa_internal.h"
 
 namespace {
 
 bool valid_dtype(int32_t dt) { return dt == FFA_DTYPE_BF16 || dt == FFA_DTYPE_FP16; }
+
+// scale: any finite value. softcap: <= 0 (none) or a finite positive cap.
+bool valid_scale(float scale, float softcap) {
+  return std::isfinite(scale) && !std::isnan(softcap) && !(softcap > 0.0f && std::isinf(softcap));
+}
 
 }  // namespace
 
@@ -24,7 +31,8 @@ const char* ffa_strerror(int status) {
     case FFA_OK:
       return "ok";
     case FFA_ERR_INVALID_ARG:
-      return "ffa: invalid argument (null pointer, non-positive size or bad stride)";
+      return "ffa: invalid argument (null pointer, non-positive size, bad stride or "
+             "non-finite scale / softcap)";
     case FFA_ERR_UNSUPPORTED_DTYPE:
       return "ffa: unsupported dtype (bfloat16 and float16; float32 for prefill)";
     case FFA_ERR_UNSUPPORTED_HEAD_DIM:
@@ -67,7 +75,7 @@ int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
       return FFA_ERR_INVALID_ARG;
     }
   }
-  if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  if (!valid_scale(a->scale, a->softcap)) return FFA_ERR_INVALID_ARG;
   // 16-byte vector / direct-to-LDS loads: aligned bases, head_dim and row strides in
   // whole 16-byte chunks.
   if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
@@ -169,7 +177,7 @@ int ffa_paged_decode_fwd(const ffa_paged_decode_args* a, void* stream) {
       return FFA_ERR_INVALID_ARG;
     }
   }
-  if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  if (!valid_scale(a->scale, a->softcap)) return FFA_ERR_INVALID_ARG;
   if (a->max_context_len > 0 && a->num_pages < 1) return FFA_ERR_INVALID_ARG;
   // 16-byte loads of q rows, K rows (to registers) and V rows (to LDS)
   if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
@@ -215,7 +223,7 @@ int ffa_mla_decode_fwd(const ffa_mla_decode_args* a, void* stream) {
       return FFA_ERR_INVALID_ARG;
     }
   }
-  if (!(a->scale == a->scale)) return FFA_ERR_INVALID_ARG;
+  if (!valid_scale(a->scale, 0.0f)) return FFA_ERR_INVALID_ARG;
   if (a->max_context_len > 0 && a->num_pages < 1) return FFA_ERR_INVALID_ARG;
   if ((reinterpret_cast<uintptr_t>(a->q) & 15u) != 0 ||
       (reinterpret_cast<uintptr_t>(a->kv_pages) & 15u) != 0) {
@@ -262,7 +270,7 @@ int ffa_attn_bwd(const ffa_attn_bwd_args* a, void* stream) {
   for (int i = 0; i < 3; ++i) {
     if (a->lse_stride[i] < 0) return FFA_ERR_INVALID_ARG;
   }
-  if (!(a->scale == a->scale) || !(a->softcap == a->softcap)) return FFA_ERR_INVALID_ARG;
+  if (!valid_scale(a->scale, a->softcap)) return FFA_ERR_INVALID_ARG;
   if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
   const void* ptrs[8] = {a->dout, a->q, a->k, a->v, a->o, a->dq, a->dk, a->dv};
   for (const void* ptr : ptrs) {

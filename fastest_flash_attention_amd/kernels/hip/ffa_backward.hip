@@ -36,6 +36,7 @@
 // head_dim up to 128.
 
 #include "ffa_common.h"
+#include "ffa_grid.h"
 #include "ffa_internal.h"
 
 namespace ffa {
@@ -82,38 +83,13 @@ struct BwdParams {
   int xcd_group_dq, xcd_group_dkv;  // > 0: units per interleaved group on one XCD
 };
 
-// Workgroup -> (unit u = batch x head, tile j; j = 0 the heaviest causal tile) for a
-// grid of n_units x n_t workgroups dealt round-robin to the 8 XCDs. With group g > 0,
-// XCD x owns units [x HX, (x + 1) HX) (HX = n_units / 8) and runs them g at a time, the
-// g units' tiles interleaved heaviest first (each unit's K/V or Q/dO stay in one L2,
-// and each group ends on light tiles); otherwise, with remap, consecutive ids share an
-// XCD (unit after unit). The same order as the forward kernel's grid.
-__device__ inline void bwd_work_item(int bid, int n_t, int g, int remap, int& u, int& j) {
-  if (g > 0) {
-    const int hx = static_cast<int>(gridDim.x / n_t) >> 3;
-    const int x = bid & 7;
-    const int k = bid >> 3;
-    const int gi = k / (g * n_t);
-    const int r = k - gi * g * n_t;
-    j = r / g;
-    u = x * hx + gi * g + (r - j * g);
-  } else {
-    if (remap) {
-      const int per_xcd = gridDim.x >> 3;
-      bid = (bid & 7) * per_xcd + (bid >> 3);
-    }
-    u = bid / n_t;
-    j = bid - u * n_t;
-  }
+// Workgroup -> (unit u = batch x head, tile j; j = 0 the heaviest causal tile): the
+// XCD-aware order of ffa_grid.h, the same as the forward kernel's grid, with the
+// group the launcher chose (bwd_xcd_group).
+__device__ inline void bwd_item(int bid, int n_t, int g, int remap, int& u, int& j) {
+  bwd_work_item(bid, static_cast<int>(gridDim.x), n_t, g, remap, u, j);
   u = __builtin_amdgcn_readfirstlane(u);
   j = __builtin_amdgcn_readfirstlane(j);
-}
-
-// Group size for a causal grid of n_units x n_t (see bwd_work_item): two units when the
-// units split evenly over the 8 XCDs in pairs and a group stays within 256 workgroups.
-int bwd_xcd_group(int causal, int64_t n_units, int n_t) {
-  if (!causal || n_units % 16 != 0 || 2 * static_cast<int64_t>(n_t) > 256) return 0;
-  return 2;
 }
 
 // XOR swizzle of the 16-byte chunk index of tile row r. Row-wise MFMA operand reads
@@ -276,7 +252,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
   const int g = lane >> 5;
 
   int bh, kt;  // causal: low key tiles are seen by the most rows (heaviest first)
-  bwd_work_item(blockIdx.x, p.n_kt, p.xcd_group_dkv, p.xcd_remap_dkv, bh, kt);
+  bwd_item(blockIdx.x, p.n_kt, p.xcd_group_dkv, p.xcd_remap_dkv, bh, kt);
   const int b = bh / p.Hkv;
   const int hk = bh - b * p.Hkv;
   const int D = p.D;
@@ -532,7 +508,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(const BwdParams p) 
   const int g = lane >> 5;
 
   int bh, jq;
-  bwd_work_item(blockIdx.x, p.n_qt, p.xcd_group_dq, p.xcd_remap_dq, bh, jq);
+  bwd_item(blockIdx.x, p.n_qt, p.xcd_group_dq, p.xcd_remap_dq, bh, jq);
   const int qt = p.causal ? (p.n_qt - 1 - jq) : jq;
   const int b = bh / p.Hq;
   const int h = bh - b * p.Hq;
@@ -812,8 +788,8 @@ int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream) {
     return FFA_ERR_TOO_LARGE;
   }
   if (grid_pre == 0 || grid_dq == 0) return FFA_OK;
-  p.xcd_remap_dq = (grid_dq % 8 == 0) ? 1 : 0;
-  p.xcd_remap_dkv = (grid_dkv % 8 == 0) ? 1 : 0;
+  p.xcd_remap_dq = bwd_xcd_remap(grid_dq);
+  p.xcd_remap_dkv = bwd_xcd_remap(grid_dkv);
   p.xcd_group_dq = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_q, p.n_qt);
   p.xcd_group_dkv = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_kv, p.n_kt);
   if (a.dtype == FFA_DTYPE_BF16) {

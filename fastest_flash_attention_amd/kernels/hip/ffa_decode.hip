@@ -23,8 +23,9 @@
 //                 one normalised (O, lse) partial per query head goes to the workspace.
 //   combine kernel one wave per (sequence, query head): O = sum_s exp(lse_s - lse) O_s,
 //                 lse = logsumexp_s lse_s.
-// Page ids outside [0, num_pages) read page 0 of the pool's first head instead of
-// faulting (their keys still count); block tables are the caller's contract.
+// Page ids outside [0, num_pages) never address memory: the tokens such a page would
+// hold are excluded from the attention like tokens past context_len (a split whose
+// staged ids are all valid pays nothing for this check).
 
 #include "ffa_common.h"
 #include "ffa_internal.h"
@@ -115,6 +116,7 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   constexpr int kRedBytes = kDecWaves * kCols * (DP + 1) * 4;
   __shared__ __attribute__((aligned(1024))) char smem[kStageBytes > kRedBytes ? kStageBytes : kRedBytes];
   __shared__ int bt_lds[kMaxSplit + 2];
+  __shared__ int bad_lds[kDecWaves];
   __shared__ float red_m[kDecWaves][kCols];
   __shared__ float red_l[kDecWaves][kCols];
   auto red_o = reinterpret_cast<float(*)[kCols][DP + 1]>(smem);
@@ -150,13 +152,20 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   const int pg0 = page_of(p, s_begin, slot0);
   int slot1;
   const int pg1 = page_of(p, s_end - 1, slot1);
+  // Invalid ids are staged as -1: loads read page 0 instead (in bounds) and the
+  // compute masks the tokens, which only splits holding such an id test (any_bad).
+  bool bad = false;
   {
     const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
     for (int i = tid; i <= pg1 - pg0; i += kDecThreads) {
       const int phys = btrow[pg0 + i];
-      bt_lds[i] = (phys >= 0 && phys < p.num_pages) ? phys : 0;
+      const bool ok = phys >= 0 && phys < p.num_pages;
+      bt_lds[i] = ok ? phys : -1;
+      bad = bad || !ok;
     }
   }
+  const bool wave_bad = __any(bad);  // every lane votes
+  if (lane == 0) bad_lds[wave] = wave_bad ? 1 : 0;
   const char* kpool = reinterpret_cast<const char*>(p.kp);
   const char* vpool = reinterpret_cast<const char*>(p.vp);
   // byte offset of token `tok` (clamped into the split) of this KV head in a pool
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
     tok = min(tok, s_end - 1);
     int slot;
     const int pg = page_of(p, tok, slot);
-    const int phys = bt_lds[pg - pg0];
+    const int phys = max(bt_lds[pg - pg0], 0);
     return (static_cast<int64_t>(phys) * p.page_stride + hk * p.head_stride +
             static_cast<int64_t>(slot) * D) * 2;
   };
@@ -186,6 +195,7 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   // explicit vmcnt waits, and no compiler wait inside the loop may count them.
   wait_vmcnt0();
   __syncthreads();  // bt_lds ready
+  const bool any_bad = (bad_lds[0] | bad_lds[1] | bad_lds[2] | bad_lds[3]) != 0;
 
   f32x4 oacc[S::DB];
 #pragma unroll
@@ -264,7 +274,12 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
         x = x * p.score_mul;
       }
       const int tok = t0 + 4 * g4 + j;
-      x = (tok < s_end) ? x : kNegInf;  // tokens below `lo` never enter a split range
+      bool live = tok < s_end;  // tokens below `lo` never enter a split range
+      if (any_bad && live) {
+        int slot;
+        live = bt_lds[page_of(p, tok, slot) - pg0] >= 0;
+      }
+      x = live ? x : kNegInf;
       sacc[j] = x;
       mt = fmaxf(mt, x);
     }
@@ -509,6 +524,7 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   static_assert(CH % 8 == 0 && kMlaTile * CH % kMlaThreads == 0, "row / tile shape");
   __shared__ __attribute__((aligned(1024))) uint16_t ring[kMlaStages][TILE];
   __shared__ int bt_lds[kMlaMaxSplit + 2];
+  __shared__ int bad_lds[kMlaWaves];
 
   // blockIdx.x = (sequence, head group), blockIdx.y = split (XCD balance, as in the
   // paged decode kernel)
@@ -534,13 +550,19 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   const int pg0 = mla_page_of(p, s_begin, slot0);
   int slot1;
   const int pg1 = mla_page_of(p, s_end - 1, slot1);
+  // invalid page ids staged as -1, read as page 0 and masked (as in the paged decode)
+  bool bad = false;
   {
     const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
     for (int i = tid; i <= pg1 - pg0; i += kMlaThreads) {
       const int phys = btrow[pg0 + i];
-      bt_lds[i] = (phys >= 0 && phys < p.num_pages) ? phys : 0;
+      const bool ok = phys >= 0 && phys < p.num_pages;
+      bt_lds[i] = ok ? phys : -1;
+      bad = bad || !ok;
     }
   }
+  const bool wave_bad = __any(bad);  // every lane votes
+  if (lane == 0) bad_lds[wave] = wave_bad ? 1 : 0;
   // Q^T as the B operand: lane holds head `head`, dims 32 ks + 8 g4 .. +7.
   u32x4 qreg[KS];
   {
@@ -554,6 +576,7 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   // Compiler-issued loads (block table, Q) complete before the asm tile loads start.
   wait_vmcnt0();
   __syncthreads();
+  const bool any_bad = (bad_lds[0] | bad_lds[1] | bad_lds[2] | bad_lds[3]) != 0;
 
   const char* pool = reinterpret_cast<const char*>(p.kv);
   const int n_tiles = (s_end - s_begin + kMlaTile - 1) / kMlaTile;
@@ -569,7 +592,7 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
       const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
       int slot;
       const int pg = mla_page_of(p, tok, slot);
-      const int64_t ro = (static_cast<int64_t>(bt_lds[pg - pg0]) * p.P + slot) * DQK * 2;
+      const int64_t ro = (static_cast<int64_t>(max(bt_lds[pg - pg0], 0)) * p.P + slot) * DQK * 2;
       load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (4 * j + wave) * 512));
     }
   };
@@ -617,7 +640,12 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tok = t0 + 16 * kb + 4 * g4 + j;
-        const float x = tok < s_end ? sacc[kb][j] * p.score_mul : kNegInf;
+        bool live = tok < s_end;
+        if (any_bad && live) {
+          int slot;
+          live = bt_lds[mla_page_of(p, tok, slot) - pg0] >= 0;
+        }
+        const float x = live ? sacc[kb][j] * p.score_mul : kNegInf;
         sacc[kb][j] = x;
         mt = fmaxf(mt, x);
       }

@@ -1,0 +1,93 @@
+// Workgroup -> work-item maps of the prefill and backward grids, and the host-side
+// choice of map for a launch. Plain integer C++: the functions are constexpr, so the
+// kernels call them on the device (clang compiles constexpr functions for host and
+// device) and tests/hip/grid_check.cpp, built by g++, checks on the CPU that every map
+// the launchers select is a bijection from workgroup ids onto (unit, tile) pairs.
+//
+// The hardware deals linear workgroup ids round-robin to the 8 XCDs of MI355X
+// (id % 8 = XCD); each XCD has its own L2, so the maps keep a unit's tiles (one
+// (batch, head): the K/V, or Q/dO, they share) on one XCD.
+#pragma once
+
+#include <stdint.h>
+
+namespace ffa {
+
+// Prefill: grid = n_units * n_qt workgroups, unit = batch x q-head, jq = query tile
+// (jq = 0 is the heaviest causal tile). With xcd_group = G > 0 (needs n_units % 8 ==
+// 0), XCD x owns units [x HX, (x + 1) HX) (HX = n_units / 8) and runs them one after
+// another, heaviest tile first, except its last min(HX, G) units, whose tiles run
+// interleaved (tile j of each in turn), so the launch ends on light tiles instead of
+// the last unit's heaviest tiles starting near the end. Without a group, xcd_remap
+// (needs grid % 8 == 0) places consecutive ids on one XCD; otherwise ids map in order.
+constexpr void prefill_work_item(int bid, int grid, int n_qt, int xcd_group, int xcd_remap,
+                                 int& unit, int& jq) {
+  if (xcd_group > 0) {
+    const int hx = (grid / n_qt) >> 3;
+    const int x = bid & 7;
+    const int k = bid >> 3;
+    const int gl = hx < xcd_group ? hx : xcd_group;
+    const int k0 = (hx - gl) * n_qt;  // tiles of the units run one after another
+    if (k < k0) {
+      const int u = k / n_qt;
+      unit = x * hx + u;
+      jq = k - u * n_qt;
+    } else {
+      const int r = k - k0;
+      jq = r / gl;
+      unit = x * hx + (hx - gl) + (r - jq * gl);
+    }
+    return;
+  }
+  if (xcd_remap) {
+    const int per_xcd = grid >> 3;
+    bid = (bid & 7) * per_xcd + (bid >> 3);
+  }
+  unit = bid / n_qt;
+  jq = bid - unit * n_qt;
+}
+
+// The prefill launcher's choice: causal grids (whose tiles differ in weight) with
+// n_units % 8 == 0 interleave the last two units of each XCD (on MI355X +2-3 % at
+// S = 8192 and +4-8 % at S = 4096 over unit after unit, for 1.26 GB of HBM reads per
+// north-star launch against 1.00; all units in interleaved pairs is as fast but reads
+// 1.51 GB, in fours 2.86 GB); other grids that split evenly over the XCDs keep
+// consecutive ids on one XCD.
+constexpr void prefill_grid_order(bool causal, int64_t n_units, int64_t grid, int& xcd_group,
+                                  int& xcd_remap) {
+  xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  xcd_group = (causal && n_units % 8 == 0) ? 2 : 0;
+}
+
+// Backward (dK/dV and dQ grids): grid = n_units * n_t, tile j = 0 the heaviest causal
+// tile. With group g > 0 (needs n_units % (8 g) == 0), XCD x owns units [x HX,
+// (x + 1) HX) and runs them g at a time, the g units' tiles interleaved heaviest first;
+// otherwise as the prefill map without a group.
+constexpr void bwd_work_item(int bid, int grid, int n_t, int g, int remap, int& unit, int& j) {
+  if (g > 0) {
+    const int hx = (grid / n_t) >> 3;
+    const int x = bid & 7;
+    const int k = bid >> 3;
+    const int gi = k / (g * n_t);
+    const int r = k - gi * g * n_t;
+    j = r / g;
+    unit = x * hx + gi * g + (r - j * g);
+    return;
+  }
+  if (remap) {
+    const int per_xcd = grid >> 3;
+    bid = (bid & 7) * per_xcd + (bid >> 3);
+  }
+  unit = bid / n_t;
+  j = bid - unit * n_t;
+}
+
+// The backward launcher's choice: causal grids whose units split evenly over the 8
+// XCDs in pairs, with a pair's tiles within 256 workgroups, run two units interleaved.
+constexpr int bwd_xcd_group(bool causal, int64_t n_units, int n_t) {
+  return (!causal || n_units % 16 != 0 || 2 * static_cast<int64_t>(n_t) > 256) ? 0 : 2;
+}
+
+constexpr int bwd_xcd_remap(int64_t grid) { return (grid % 8 == 0) ? 1 : 0; }
+
+}  // namespace ffa

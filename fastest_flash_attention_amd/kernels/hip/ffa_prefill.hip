@@ -33,6 +33,7 @@
 #include <type_traits>
 
 #include "ffa_common.h"
+#include "ffa_grid.h"
 #include "ffa_internal.h"
 #include "ffa_prefill_common.h"
 
@@ -47,40 +48,10 @@ constexpr int kBlockM = 128;
 // its rows and visits only those; sweeps longer than this many tiles visit every tile.
 constexpr int kMaxLiveTiles = 2048;
 constexpr int kTileFull = 0x8000;  // list entry flag: the block mask keeps the whole tile
-// Workgroup -> (batch x head, query tile j; j = 0 is the heaviest causal tile). The
-// hardware deals linear workgroup ids round-robin to the 8 XCDs. With xcd_group = G,
-// XCD x owns heads [x HX, (x + 1) HX) (HX = B Hq / 8) and runs them head after head,
-// heaviest tile first, so each head's K/V stay in one L2 while its tiles run; only its
-// last G heads run interleaved (tile j of each in turn), so the launch ends on light
-// tiles instead of the last head's heaviest tiles starting near the end. Causal
-// launches use G = 2: on MI355X +2-3 % at S = 8192 and +4-8 % at S = 4096 over plain
-// head after head, for 1.26 GB of HBM reads per north-star launch against 1.00 (all
-// heads in interleaved pairs: same speed, 1.51 GB; in fours: 2.86 GB). Without
-// xcd_group, xcd_remap places consecutive ids on one XCD.
+// Workgroup -> (batch x head, query tile j; j = 0 is the heaviest causal tile): the
+// XCD-aware order of ffa_grid.h, with the group / remap the launcher chose.
 __device__ inline void work_item(const PrefillParams& p, int bid, int& bh, int& jq) {
-  if (p.xcd_group > 0) {
-    const int hx = static_cast<int>(gridDim.x / p.n_qt) >> 3;
-    const int x = bid & 7;
-    const int k = bid >> 3;
-    const int gl = min(hx, p.xcd_group);
-    const int k0 = (hx - gl) * p.n_qt;  // tiles of the heads run one after another
-    if (k < k0) {
-      const int u = k / p.n_qt;
-      bh = x * hx + u;
-      jq = k - u * p.n_qt;
-    } else {
-      const int r = k - k0;
-      jq = r / gl;
-      bh = x * hx + (hx - gl) + (r - jq * gl);
-    }
-    return;
-  }
-  if (p.xcd_remap) {
-    const int per_xcd = gridDim.x >> 3;
-    bid = (bid & 7) * per_xcd + (bid >> 3);
-  }
-  bh = bid / p.n_qt;
-  jq = bid - bh * p.n_qt;
+  prefill_work_item(bid, static_cast<int>(gridDim.x), p.n_qt, p.xcd_group, p.xcd_remap, bh, jq);
 }
 
 template <int DP, int BN>
@@ -300,13 +271,16 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
 
   // Q^T as the B operand: lane holds row qrow (clamped: rows past Sq are never
   // stored), dims 16*ks + 8g .. +7.
+  // A negative scale is applied as q.k * scale = (-q).k * |scale|: the sign bits of Q
+  // are flipped here (exact), so the kernel's multiplier stays positive.
   u32x4 qreg[S::KS];
   {
     const uint16_t* qr = qbase + static_cast<int64_t>(min(qrow, p.Sq - 1)) * p.q_ss;
+    const uint32_t qx = p.q_neg ? 0x80008000u : 0u;
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
       const int d0 = min(16 * ks + 8 * g, D - 8);
-      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + d0);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + d0) ^ qx;
       qreg[ks] = (16 * ks + 8 * g < D) ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
@@ -684,7 +658,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillP
       f32x4 v = {0.f, 0.f, 0.f, 0.f};
       if (d0 < D) v = *reinterpret_cast<const f32x4*>(qr + d0);  // D % 8 == 0
 #pragma unroll
-      for (int e = 0; e < 4; ++e) qreg[c4 + e] = v[e];
+      for (int e = 0; e < 4; ++e) qreg[c4 + e] = p.q_neg ? -v[e] : v[e];  // negative scale
     }
   }
   f32x16 oacc[DB];
@@ -858,11 +832,26 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   p.ratio = a.heads_q / a.heads_kv;
   p.n_qt = (a.seqlen_q + kBlockM - 1) / kBlockM;
   const bool softcap = a.softcap > 0.0f;
+  // Without softcap the kernels keep the running max of raw q.k, so their multiplier
+  // must be positive: a negative scale flips Q's sign instead (q.k * scale =
+  // (-q).k * |scale|), and a zero or tiny scale becomes 1e-30, which rounds every
+  // exponent q.k * 1e-30 * log2 e (|q.k| < 1e20) to 0: the uniform softmax with
+  // LSE = log(n) that scale 0 gives. With softcap the scores are tanh-transformed
+  // before the max (tanh is odd), so any finite scale is used as it is.
+  float scale = a.scale;
+  p.q_neg = 0;
+  if (!softcap) {
+    if (scale < 0.0f) {
+      scale = -scale;
+      p.q_neg = 1;
+    }
+    scale = fmaxf(scale, 1e-30f);
+  }
   if (softcap) {
-    p.score_mul = a.scale / a.softcap;
+    p.score_mul = scale / a.softcap;
     p.cap_mul = a.softcap * kLog2e;
   } else {
-    p.score_mul = a.scale * kLog2e;
+    p.score_mul = scale * kLog2e;
     p.cap_mul = 0.0f;
   }
   p.ref_bq = a.ref_block_q > 0 ? a.ref_block_q : 64;
@@ -879,10 +868,8 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   if (grid64 <= 0) return FFA_OK;
   if (grid64 > 0x7fffffff) return FFA_ERR_TOO_LARGE;
   const int grid = static_cast<int>(grid64);
-  p.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  // non-causal tiles weigh the same: no tail to avoid
-  const int64_t nbh = static_cast<int64_t>(a.batch) * a.heads_q;
-  p.xcd_group = (p.causal && nbh % 8 == 0) ? 2 : 0;
+  prefill_grid_order(p.causal != 0, static_cast<int64_t>(a.batch) * a.heads_q, grid,
+                     p.xcd_group, p.xcd_remap);
 
   if (a.dtype == FFA_DTYPE_BF16) {
     launch_tag<Bf16Tag>(p, softcap, grid, stream);

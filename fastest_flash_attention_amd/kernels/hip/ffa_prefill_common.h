@@ -26,6 +26,7 @@ struct PrefillParams {
   int n_qt;
   float score_mul;  // scale*log2e, or scale/softcap with softcap
   float cap_mul;    // softcap*log2e (softcap only)
+  uint32_t q_neg;   // 1: Q's sign bits are flipped as it is loaded (negative scale)
   int ref_bq, ref_bkv;
   int masked_lse_mode;
   int xcd_remap;

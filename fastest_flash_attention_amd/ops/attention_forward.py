@@ -247,18 +247,6 @@ def build_prefill_args(
     return a
 
 
-def _positive_scale(q: torch.Tensor, scale: float) -> Tuple[torch.Tensor, float]:
-    """The kernels keep the running max of raw scores q.k and need scale > 0. A negative
-    scale is applied exactly as q.k.scale = (-q).k.|scale| (a negated copy of q); a zero
-    scale becomes 1e-30, which gives exp2(q.k * 1e-30 * log2 e) = 1 in fp32 for every
-    |q.k| < 1e20, i.e. the uniform softmax the reference computes."""
-    if scale < 0:
-        return torch.neg(q), -scale
-    if scale == 0:
-        return q, 1e-30
-    return q, scale
-
-
 def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> PrefillCall:
     """Resolve arguments, check device/dtype/features, allocate outputs, build the ABI
     struct. Launches nothing."""
@@ -288,7 +276,6 @@ def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> Pref
             raise TypeError(f"unsupported compute_dtype {r.compute_dtype}")
     if r.D > 256:
         raise ValueError(f"head_dim {r.D} > 256 is not supported")
-    r.q, r.scale = _positive_scale(r.q, r.scale)
     d_pad = (r.D + 7) // 8 * 8
     r.q = _conform(r.q, d_pad)
     r.k = _conform(r.k, d_pad)

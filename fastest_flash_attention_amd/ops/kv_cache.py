@@ -13,8 +13,14 @@ split-K HIP kernel ``ffa_paged_decode_fwd``. ``append_tokens`` (the write path) 
 its semantics but writes all new tokens with one indexed copy instead of a
 per-token loop.
 
-The read path runs on ROCm tensors only; a CPU pool can be filled and inspected
-but not read through ``get_kv`` / ``decode``.
+Decode runs on ROCm tensors only. A pool in host memory (the constructor's
+default device, as in the reference) is filled by ``append_tokens`` and read by
+``get_kv`` with indexed host copies, which move data and compute nothing.
+
+Page ids outside the pool never address memory in the kernels: decode excludes the
+tokens such an id would hold (see include/ffa.h). ``check_block_tables=True``
+restores the reference's IndexError (ops/kv_cache.py:226-227) at the cost of one
+device reduction and a host sync.
 """
 
 from __future__ import annotations
@@ -26,7 +32,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from ..kernels import _lib
-from .attention_forward import _positive_scale
+from .attention_forward import launch_prefill, prepare_prefill
 
 
 def _auto_tokens_per_split(batch: int, heads_kv: int, max_len: int) -> int:
@@ -40,6 +46,73 @@ def _auto_tokens_per_split(batch: int, heads_kv: int, max_len: int) -> int:
     while tps > 64 and batch * heads_kv * max(1, math.ceil(max_len / tps)) < 256:
         tps //= 2
     return tps
+
+
+def check_page_ids(block_tables: torch.Tensor, context_lens: torch.Tensor, page_size: int,
+                   num_pages: int, max_context_len: int) -> None:
+    """Raise IndexError if a page id the lengths reach lies outside ``[0, num_pages)``:
+    entry j of row b is used when ``j * page_size < min(context_lens[b],
+    max_context_len)``. One device reduction and a host sync."""
+    if block_tables.numel() == 0:
+        return
+    lens = torch.clamp(context_lens.to(torch.int64), min=0, max=max_context_len)
+    used = (torch.arange(block_tables.size(1), device=block_tables.device)[None, :] * page_size
+            < lens[:, None])
+    bad = used & ((block_tables < 0) | (block_tables >= num_pages))
+    if bool(bad.any()):
+        b, j = (int(x) for x in bad.nonzero()[0])
+        raise IndexError(f"block_tables[{b}, {j}] = {int(block_tables[b, j])} is outside the "
+                         f"pool of {num_pages} pages")
+
+
+def _paged_decode_fp32(q3, k_pages, v_pages, block_tables, context_lens, scale, softcap,
+                       sliding_window, return_lse, max_context_len):
+    """Decode over fp32 pools: per sequence, ``ffa_paged_gather`` of its pages and one
+    ``ffa_prefill_fwd`` on the fp32 MFMA kernel with the query at position L - 1 (the
+    reference's get_kv + forward, ops/kv_cache.py:208-232, in fp32 as it computes).
+    Two launches per sequence instead of the batched split-K kernels, which take
+    16-bit pools; page ids are always checked (IndexError)."""
+    B, Hq, D = q3.shape
+    P_total, Hkv, page_size, _ = k_pages.shape
+    lens = context_lens.to(torch.int64).clamp(min=0).tolist()
+    if max_context_len is not None:
+        lens = [min(n, int(max_context_len)) for n in lens]
+    bt = block_tables.to(torch.int32).contiguous()
+    check_page_ids(bt, context_lens, page_size, P_total, max(lens + [0]))
+    out = torch.zeros((B, Hq, D), dtype=torch.float32, device=q3.device)
+    lse = (torch.full((B, Hq), float("-inf"), dtype=torch.float32, device=q3.device)
+           if return_lse else None)
+    lib = _lib.load()
+    stream = _lib.current_stream_handle(q3.device)
+    for b, L in enumerate(lens):
+        if L == 0:
+            continue
+        k = torch.empty(Hkv, L, D, dtype=torch.float32, device=q3.device)
+        v = torch.empty_like(k)
+        g = _lib.PagedGatherArgs()
+        g.k_pages = k_pages.data_ptr()
+        g.v_pages = v_pages.data_ptr()
+        g.k_out = k.data_ptr()
+        g.v_out = v.data_ptr()
+        g.page_table = bt[b].data_ptr()
+        g.num_pages = P_total
+        g.heads_kv = Hkv
+        g.page_size = page_size
+        g.head_dim = D
+        g.context_len = L
+        g.elem_bytes = 4
+        with torch.cuda.device(q3.device):
+            _lib.check(lib.ffa_paged_gather(ctypes.byref(g), ctypes.c_void_p(stream)))
+        call = prepare_prefill(q3[b, :, None, :].unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                               scale=scale, causal=True, softcap=softcap,
+                               sliding_window=sliding_window, num_kv_heads=Hkv,
+                               return_lse=return_lse)
+        call.args.q_offset = L - 1  # the query is the sequence's last token
+        launch_prefill(call)
+        out[b] = call.out[0, :, 0, :D]
+        if lse is not None:
+            lse[b] = call.lse[0, :, 0, 0]
+    return out, lse
 
 
 def decode_workspace_bytes(batch: int, heads_q: int, head_dim: int, max_context_len: int,
@@ -62,8 +135,14 @@ def fastest_flash_paged_decode(
     max_context_len: Optional[int] = None,
     tokens_per_split: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
+    check_block_tables: bool = False,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """One decode step for a batch of paged sequences.
+
+    Page ids outside ``[0, num_pages)`` in the first ``ceil(L_b / page_size)`` entries
+    of a row exclude the tokens they would hold (the kernels never read through them);
+    with ``check_block_tables=True`` they raise IndexError instead, as the reference's
+    page indexing does (ops/kv_cache.py:226-227).
 
     q: ``[B, Hq, D]`` or ``[B, Hq, 1, D]``; k_pages/v_pages: ``[P, Hkv, page_size, D]``
     (PagedKVCache layout); block_tables: int32 ``[B, max_blocks]``; context_lens: int32
@@ -100,6 +179,15 @@ def fastest_flash_paged_decode(
             )
     if not (q3.dtype == k_pages.dtype == v_pages.dtype):
         raise TypeError("q and the page pools must share a dtype")
+    if q3.dtype == torch.float32:
+        out, lse = _paged_decode_fp32(q3, k_pages, v_pages, block_tables, context_lens,
+                                      scale, softcap, sliding_window, return_lse,
+                                      max_context_len)
+        if not squeeze:
+            out = out.unsqueeze(2)
+            if lse is not None:
+                lse = lse[:, :, None, None]
+        return out, lse
     code = _lib.dtype_code(q3.dtype)
     if D % 8 != 0:
         raise ValueError(f"paged decode needs head_dim % 8 == 0 (got {D})")
@@ -115,9 +203,10 @@ def fastest_flash_paged_decode(
         max_context_len = int(context_lens.max().item()) if B > 0 else 0
     if block_tables.size(1) * page_size < max_context_len:
         raise ValueError("block_tables has fewer columns than max_context_len needs")
+    if check_block_tables:
+        check_page_ids(block_tables, context_lens, page_size, P_total, max_context_len)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    q3, scale = _positive_scale(q3, float(scale))
     if sliding_window is not None and int(sliding_window) <= 0:
         raise ValueError("sliding_window must be positive")
     if softcap is not None and float(softcap) <= 0.0:
@@ -356,16 +445,30 @@ class PagedKVCache:
         return torch.tensor(self.sequences[seq_id]["page_table"], dtype=torch.int32,
                             device=self.k_pages.device)
 
+    def _get_kv_host(self, seq_id: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """``get_kv`` of a pool in host memory (the constructor's default device): one
+        indexed copy by the index law, token t from (page_table[t // P], t % P). It is a
+        data copy of the cache the caller keeps on the host, like the reference's
+        per-page slice copies (:224-230), bit-identical to them; no attention runs."""
+        seq = self.sequences[seq_id]
+        L = seq["len"]
+        P = self.page_size
+        t = torch.arange(L, dtype=torch.int64)
+        table = torch.tensor(seq["page_table"], dtype=torch.int64)
+        phys, slot = table[t // P], t % P
+        # advanced indices on dims 0 and 2 put the token dim first: [L, H, D] -> [H, L, D]
+        k_out = self.k_pages[phys, :, slot, :].transpose(0, 1).contiguous()
+        v_out = self.v_pages[phys, :, slot, :].transpose(0, 1).contiguous()
+        return k_out, v_out
+
     def get_kv(self, seq_id: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """Contiguous ``([H, L, D], [H, L, D])`` of a sequence, or ``(None, None)``
-        (reference :208-232), gathered by one ``ffa_paged_gather`` launch."""
+        (reference :208-232). A ROCm pool is gathered by one ``ffa_paged_gather``
+        launch; a host pool by one indexed host copy."""
         if seq_id not in self.sequences or self.sequences[seq_id]["len"] == 0:
             return None, None
         if self.k_pages.device.type != "cuda":
-            raise RuntimeError(
-                "PagedKVCache.get_kv runs on ROCm pools only (create the cache with "
-                "device='cuda'); there is no CPU read path"
-            )
+            return self._get_kv_host(seq_id)
         if self.k_pages.element_size() not in (2, 4):
             raise TypeError(f"unsupported pool dtype {self.k_pages.dtype}")
         L = self.sequences[seq_id]["len"]

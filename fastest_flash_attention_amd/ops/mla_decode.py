@@ -25,7 +25,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from ..kernels import _lib
-from .attention_forward import _positive_scale
+from .kv_cache import check_page_ids
 
 MLA_ROPE_DIM = 64
 MLA_LATENT_DIMS = (256, 512)
@@ -59,8 +59,12 @@ def fastest_flash_mla_decode(
     max_context_len: Optional[int] = None,
     tokens_per_split: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
+    check_block_tables: bool = False,
 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Latent-space attention of one query token per sequence.
+
+    Page ids outside the pool exclude the tokens they would hold, or raise IndexError
+    with ``check_block_tables=True`` (as for ``fastest_flash_paged_decode``).
 
     q: ``[B, H, dim_v + 64]`` absorbed queries ``[W_uk^T q_nope, q_rope]``; kv_pages:
     ``[num_pages, page_size, dim_v + 64]`` rows ``[c_t | r_t]``; block_tables int32
@@ -94,9 +98,10 @@ def fastest_flash_mla_decode(
         max_context_len = int(context_lens.max().item()) if B > 0 else 0
     if block_tables.size(1) * page_size < max_context_len:
         raise ValueError("block_tables has fewer columns than max_context_len needs")
+    if check_block_tables:
+        check_page_ids(block_tables, context_lens, page_size, num_pages, max_context_len)
     if tokens_per_split is None:
         tokens_per_split = _auto_mla_tokens_per_split(B, (H + 31) // 32, max_context_len)
-    q, scale = _positive_scale(q, float(scale))
 
     lib = _lib.load()
     out = torch.empty((B, H, dim_v), dtype=q.dtype, device=q.device)

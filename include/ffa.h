@@ -48,11 +48,12 @@
 extern "C" {
 #endif
 
-#define FFA_ABI_VERSION 4
+#define FFA_ABI_VERSION 5
 
 typedef enum ffa_status {
   FFA_OK = 0,
-  FFA_ERR_INVALID_ARG = -1,      /* null pointer, non-positive size, bad stride, ... */
+  FFA_ERR_INVALID_ARG = -1,      /* null pointer, non-positive size, bad stride,
+                                    non-finite scale or softcap, ... */
   FFA_ERR_UNSUPPORTED_DTYPE = -2,
   FFA_ERR_UNSUPPORTED_HEAD_DIM = -3,
   FFA_ERR_MISALIGNED = -4,       /* base not 16-byte aligned, or head_dim / a stride not a
@@ -74,7 +75,10 @@ typedef enum ffa_dtype {
  * Prefill / general forward attention.
  *
  * Semantics (kernels/cpu_reference.py:132-312, ops/attention_forward.py:23-167):
- *   S      = (q . k^T) * scale                       fp32 accumulation
+ *   S      = (q . k^T) * scale                       fp32 accumulation; scale is any
+ *            finite value, as the replaced launchers accept (a negative scale gives
+ *            the softmax of the negated scores, zero the uniform softmax over the
+ *            visible keys with lse = log(n)); a non-finite scale is FFA_ERR_INVALID_ARG
  *   S      = softcap * tanh(S / softcap)              if softcap > 0, before masking
  *   masked : key >= seqlen_kv,
  *            causal && key > q_offset + row,          (top-left aligned when q_offset=0)
@@ -118,8 +122,8 @@ typedef struct ffa_prefill_args {
   int32_t q_offset;         /* absolute position of query row 0 */
   int32_t causal;           /* 0 / 1 */
   int32_t window;           /* <= 0: no sliding window */
-  float scale;
-  float softcap;            /* <= 0: no softcap */
+  float scale;              /* any finite value */
+  float softcap;            /* <= 0: no softcap; else finite */
   int32_t ref_block_q;      /* reference tile sizes: only used for the LSE sentinel */
   int32_t ref_block_kv;     /*   of rows with no visible key; <= 0 means 64 */
   int32_t masked_lse_mode;  /* 0: one-pass sentinel log(n*1e-30); 1: -inf (the
@@ -138,6 +142,13 @@ int ffa_prefill_fwd(const ffa_prefill_args* args, void* stream);
  *   k_pages, v_pages : [num_pages, heads_kv, page_size, head_dim], contiguous.
  * Index law (ops/kv_cache.py:194-203): token t of sequence b lives in physical
  * page block_tables[b * block_table_stride + t / page_size], slot t % page_size.
+ * Page ids outside [0, num_pages) never address memory. The reference raises
+ * IndexError for them (ops/kv_cache.py:226-227); here, in the decode entry points,
+ * the tokens such an id would hold are excluded from the attention, exactly like
+ * tokens past context_len (a sequence left with no token gets O = 0, lse = -inf);
+ * ffa_paged_gather writes zeros for them and ffa_paged_append skips them. Callers
+ * that want the reference's error check the ids first (the Python layer offers
+ * that check as an option).
  */
 
 /* Gather sequence pages into contiguous [heads_kv, context_len, head_dim] (get_kv). */
@@ -230,9 +241,9 @@ typedef struct ffa_paged_decode_args {
   int32_t max_context_len;       /* upper bound of context_lens (sizes the grid) */
   int32_t tokens_per_split;      /* 0: library default */
   int32_t window;                /* <= 0: none */
-  float scale;
-  float softcap;                 /* <= 0: none */
-  int32_t dtype;                 /* ffa_dtype */
+  float scale;                   /* any finite value */
+  float softcap;                 /* <= 0: none; else finite */
+  int32_t dtype;                 /* FFA_DTYPE_BF16 or FFA_DTYPE_FP16 */
 } ffa_paged_decode_args;
 
 /* Split count per sequence the decode entry point uses for these sizes. */
@@ -282,7 +293,7 @@ typedef struct ffa_mla_decode_args {
   int32_t num_pages;
   int32_t max_context_len;
   int32_t tokens_per_split;      /* 0: library default */
-  float scale;
+  float scale;                   /* any finite value */
   int32_t dtype;                 /* FFA_DTYPE_BF16 or FFA_DTYPE_FP16 */
 } ffa_mla_decode_args;
 

@@ -104,10 +104,12 @@ def test_product_path_refuses_cpu_and_unsupported():
         af.prepare_prefill(q, q, q, block_mask=torch.ones(1, 1, dtype=torch.bool))
     with pytest.raises(RuntimeError, match="ROCm GPU tensors only"):
         af.prepare_prefill(q, q, q, compute_dtype=torch.float16)
+    # a host pool is read by get_kv (a copy), but decode attention needs the GPU
     cache = ffa.PagedKVCache(max_pages=4, page_size=4, num_heads=1, head_dim=8)
     cache.append_tokens(0, torch.randn(1, 3, 8), torch.randn(1, 3, 8))
+    assert cache.get_kv(0)[0].shape == (1, 3, 8)
     with pytest.raises(RuntimeError, match="ROCm"):
-        cache.get_kv(0)
+        cache.decode(torch.randn(1, 1, 8, dtype=torch.float16), [0])
 
 
 # ---------------------------------------------------------------------------------
@@ -307,3 +309,111 @@ def test_auto_tokens_per_split():
     assert _auto_tokens_per_split(4, 8, 8192) == 1024    # 4*8*8 = 256 workgroups
     assert _auto_tokens_per_split(1, 8, 4096) == 128     # 1*8*32 = 256 workgroups
     assert _auto_tokens_per_split(1, 1, 100) == 64       # tiny problem: shortest split
+
+
+def _valid_prefill_args(scale, softcap=0.0):
+    """Sizes, strides and (fake, aligned) pointers that pass every host check up to the
+    scale, so the returned code is decided by scale / softcap alone."""
+    a = _lib.PrefillArgs()
+    a.q = a.k = a.v = a.o = 16
+    st = [4 * 64 * 64, 64 * 64, 64, 1]
+    a.q_stride[:] = a.k_stride[:] = a.v_stride[:] = a.o_stride[:] = st
+    a.batch, a.heads_q, a.heads_kv, a.seqlen_q, a.seqlen_kv, a.head_dim = 1, 4, 4, 64, 64, 64
+    a.dtype, a.scale, a.softcap = _lib.FFA_DTYPE_BF16, scale, softcap
+    return a
+
+
+@pytest.mark.parametrize("scale,softcap", [
+    (float("inf"), 0.0), (float("-inf"), 0.0), (float("nan"), 0.0),
+    (0.125, float("nan")), (0.125, float("inf")),
+])
+def test_abi_rejects_non_finite_scale(lib, scale, softcap):
+    """The C ABI takes any finite scale (negative and zero included: the library applies
+    them, see the GPU tests) and rejects non-finite ones before any HIP call."""
+    a = _valid_prefill_args(scale, softcap)
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -1
+    d = _lib.PagedDecodeArgs()
+    d.dtype, d.head_dim, d.batch, d.heads_q, d.heads_kv, d.page_size = 0, 128, 2, 8, 2, 16
+    d.max_context_len, d.block_table_stride, d.num_pages = 64, 4, 8
+    d.q = d.o = d.k_pages = d.v_pages = d.block_tables = d.context_lens = 16
+    d.scale, d.softcap = scale, softcap
+    assert lib.ffa_paged_decode_fwd(ctypes.byref(d), None) == -1
+    if softcap == 0.0:
+        m = _lib.MlaDecodeArgs()
+        m.dtype, m.dim_v, m.dim_rope, m.batch, m.heads_q, m.page_size = 0, 512, 64, 2, 32, 16
+        m.max_context_len, m.block_table_stride, m.num_pages = 64, 4, 8
+        m.q = m.o = m.kv_pages = m.block_tables = m.context_lens = 16
+        m.scale = scale
+        assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -1
+
+
+def test_host_layer_passes_scale_unchanged():
+    """Negative and zero scales reach the ABI struct as given: the library, not the
+    Python layer, owns their meaning (ops/attention_forward.py:98-99 passes any value)."""
+    q = torch.randn(1, 2, 8, 16)
+    for s in (-0.25, 0.0, 0.5):
+        r = af.resolve_forward_args(q, q, q, scale=s)
+        out = torch.empty(1, 2, 8, 16)
+        a = af.build_prefill_args(r, out, None, _lib.FFA_DTYPE_BF16)
+        assert a.scale == s and a.q == q.data_ptr()
+
+
+# ---------------------------------------------------------------------------------
+# PagedKVCache read path of a host pool (the constructor's default device)
+# ---------------------------------------------------------------------------------
+
+def test_reference_paged_basic_flow():
+    """The reference's own test_paged_basic (tests/test_fastest_flash.py:398-411): an fp32
+    pool on the default device, append then get_kv."""
+    cache = ffa.PagedKVCache(max_pages=16, page_size=4, num_heads=2, head_dim=8,
+                             dtype=torch.float32)
+    k = torch.randn(2, 6, 8)
+    v = torch.randn(2, 6, 8)
+    assert cache.append_tokens(0, k, v) == 6
+    k_out, v_out = cache.get_kv(0)
+    assert k_out.shape == (2, 6, 8)
+    assert torch.allclose(k_out, k) and torch.allclose(v_out, v)
+    assert cache.get_kv(1) == (None, None)
+
+
+def test_host_get_kv_matches_reference_page_copies():
+    """get_kv on a host pool equals the reference's per-page slice copies
+    (ops/kv_cache.py:224-230, restated by oracle.paged.gather_sequence) bit for bit,
+    across sequences that interleave their pages and a freed-and-reused page."""
+    gen = torch.Generator().manual_seed(3)
+    cache = ffa.PagedKVCache(max_pages=10, page_size=3, num_heads=3, head_dim=5,
+                             dtype=torch.float16)
+    pool = opaged.PagedPool(max_pages=10, page_size=3, num_heads=3, head_dim=5,
+                            dtype=np.float16)
+    for sid, n in ((0, 4), (1, 2), (0, 5), (2, 7)):
+        k = torch.randn(3, n, 5, generator=gen).half()
+        v = torch.randn(3, n, 5, generator=gen).half()
+        cache.append_tokens(sid, k, v)
+        pool.append_tokens(sid, k.numpy(), v.numpy())
+    cache.free_sequence(1)
+    pool.free_sequence(1)
+    k = torch.randn(3, 4, 5, generator=gen).half()
+    cache.append_tokens(3, k, k)
+    pool.append_tokens(3, k.numpy(), k.numpy())
+    for sid in (0, 2, 3):
+        ko, vo = cache.get_kv(sid)
+        seq = pool.sequences[sid]
+        rk, rv = opaged.gather_sequence(pool.k_pages, pool.v_pages, seq["page_table"], seq["len"])
+        assert ko.dtype == torch.float16 and ko.is_contiguous()
+        assert np.array_equal(ko.numpy(), rk) and np.array_equal(vo.numpy(), rv)
+
+
+def test_check_page_ids():
+    from fastest_flash_attention_amd.ops.kv_cache import check_page_ids
+
+    # pool of 8 pages, 4 tokens per page: entry j of a row is used while 4 j < length
+    bt = torch.tensor([[3, 1, 7], [2, 9, -1]], dtype=torch.int32)
+    check_page_ids(bt, torch.tensor([9, 4], dtype=torch.int32), 4, 8, 9)  # unused 9, -1 pass
+    with pytest.raises(IndexError, match=r"block_tables\[1, 1\] = 9"):
+        check_page_ids(bt, torch.tensor([9, 5], dtype=torch.int32), 4, 8, 9)
+    check_page_ids(bt, torch.tensor([9, 5], dtype=torch.int32), 4, 8, 4)  # clamped length
+    with pytest.raises(IndexError, match=r"block_tables\[1, 2\] = -1"):
+        check_page_ids(torch.tensor([[3, 1, 7], [2, 5, -1]], dtype=torch.int32),
+                       torch.tensor([0, 12], dtype=torch.int32), 4, 8, 12)
+    with pytest.raises(IndexError):
+        check_page_ids(bt, torch.tensor([9, 0], dtype=torch.int32), 4, 7, 9)  # 7 >= 7 pages
