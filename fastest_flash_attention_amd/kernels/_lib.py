@@ -24,6 +24,7 @@ FFA_ABI_VERSION = 5
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
 FFA_DTYPE_FP32 = 2
+FFA_NOALLOC_SCRATCH_BYTES = 64 << 20  # include/ffa.h
 
 _I64x4 = ctypes.c_int64 * 4
 _I64x3 = ctypes.c_int64 * 3
@@ -215,6 +216,9 @@ EXPORTS = {
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],
     ),
     "ffa_paged_decode_fwd": (ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), ctypes.c_void_p]),
+    "ffa_paged_decode_fwd_noalloc": (
+        ctypes.c_int, [ctypes.POINTER(PagedDecodeArgs), ctypes.c_void_p],
+    ),
     "ffa_mla_decode_workspace_bytes": (
         ctypes.c_size_t,
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32],

@@ -20,6 +20,46 @@ bool valid_scale(float scale, float softcap) {
   return std::isfinite(scale) && !std::isnan(softcap) && !(softcap > 0.0f && std::isinf(softcap));
 }
 
+// Every check of a paged decode call except its workspace. *empty: nothing to launch.
+int check_decode_args(const ffa_paged_decode_args* a, bool* empty) {
+  *empty = false;
+  if (a == nullptr) return FFA_ERR_INVALID_ARG;
+  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->page_size < 1 ||
+      a->num_pages < 0 || a->max_context_len < 0 || a->tokens_per_split < 0) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  if (a->heads_q % a->heads_kv != 0) return FFA_ERR_GQA_RATIO;
+  if (a->heads_q / a->heads_kv > 64) return FFA_ERR_GQA_RATIO;
+  if (a->batch == 0) {
+    *empty = true;
+    return FFA_OK;
+  }
+  if (a->q == nullptr || a->o == nullptr || a->k_pages == nullptr || a->v_pages == nullptr ||
+      a->block_tables == nullptr || a->context_lens == nullptr) {
+    return FFA_ERR_INVALID_ARG;
+  }
+  const int64_t max_blocks =
+      (static_cast<int64_t>(a->max_context_len) + a->page_size - 1) / a->page_size;
+  if (a->block_table_stride < max_blocks) return FFA_ERR_INVALID_ARG;
+  for (int i = 0; i < 2; ++i) {
+    if (a->q_stride[i] < 0 || a->o_stride[i] < 0 || a->lse_stride[i] < 0) {
+      return FFA_ERR_INVALID_ARG;
+    }
+  }
+  if (!valid_scale(a->scale, a->softcap)) return FFA_ERR_INVALID_ARG;
+  if (a->max_context_len > 0 && a->num_pages < 1) return FFA_ERR_INVALID_ARG;
+  // 16-byte loads of q rows, K rows (to registers) and V rows (to LDS)
+  if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
+  const void* ptrs[3] = {a->q, a->k_pages, a->v_pages};
+  for (const void* ptr : ptrs) {
+    if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) return FFA_ERR_MISALIGNED;
+  }
+  if (a->q_stride[0] % 8 != 0 || a->q_stride[1] % 8 != 0) return FFA_ERR_MISALIGNED;
+  return FFA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -50,6 +90,10 @@ const char* ffa_strerror(int status) {
       return "ffa: no usable HIP device";
     case FFA_ERR_TOO_LARGE:
       return "ffa: problem size exceeds 32-bit grid/index limits";
+    case FFA_ERR_SCRATCH_LIMIT:
+      return "ffa: the split-K partials of this call exceed the allocation-free entry point's "
+             "static scratch (FFA_NOALLOC_SCRATCH_BYTES); use ffa_paged_decode_fwd with a "
+             "workspace, or longer splits";
     default:
       return "ffa: unknown error";
   }
@@ -155,42 +199,21 @@ size_t ffa_paged_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t 
 }
 
 int ffa_paged_decode_fwd(const ffa_paged_decode_args* a, void* stream) {
-  if (a == nullptr) return FFA_ERR_INVALID_ARG;
-  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
-  if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
-  if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->page_size < 1 ||
-      a->num_pages < 0 || a->max_context_len < 0 || a->tokens_per_split < 0) {
-    return FFA_ERR_INVALID_ARG;
-  }
-  if (a->heads_q % a->heads_kv != 0) return FFA_ERR_GQA_RATIO;
-  if (a->heads_q / a->heads_kv > 64) return FFA_ERR_GQA_RATIO;
-  if (a->batch == 0) return FFA_OK;
-  if (a->q == nullptr || a->o == nullptr || a->k_pages == nullptr || a->v_pages == nullptr ||
-      a->block_tables == nullptr || a->context_lens == nullptr) {
-    return FFA_ERR_INVALID_ARG;
-  }
-  const int64_t max_blocks =
-      (static_cast<int64_t>(a->max_context_len) + a->page_size - 1) / a->page_size;
-  if (a->block_table_stride < max_blocks) return FFA_ERR_INVALID_ARG;
-  for (int i = 0; i < 2; ++i) {
-    if (a->q_stride[i] < 0 || a->o_stride[i] < 0 || a->lse_stride[i] < 0) {
-      return FFA_ERR_INVALID_ARG;
-    }
-  }
-  if (!valid_scale(a->scale, a->softcap)) return FFA_ERR_INVALID_ARG;
-  if (a->max_context_len > 0 && a->num_pages < 1) return FFA_ERR_INVALID_ARG;
-  // 16-byte loads of q rows, K rows (to registers) and V rows (to LDS)
-  if (a->head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
-  const void* ptrs[3] = {a->q, a->k_pages, a->v_pages};
-  for (const void* ptr : ptrs) {
-    if ((reinterpret_cast<uintptr_t>(ptr) & 15u) != 0) return FFA_ERR_MISALIGNED;
-  }
-  if (a->q_stride[0] % 8 != 0 || a->q_stride[1] % 8 != 0) return FFA_ERR_MISALIGNED;
+  bool empty = false;
+  const int rc = check_decode_args(a, &empty);
+  if (rc != FFA_OK || empty) return rc;
   const size_t need = ffa::decode_workspace_bytes(a->batch, a->heads_q, a->head_dim,
                                                   a->max_context_len, a->tokens_per_split);
   if (need > 0 && (a->workspace == nullptr || a->workspace_bytes < need)) return FFA_ERR_WORKSPACE;
   if ((reinterpret_cast<uintptr_t>(a->workspace) & 15u) != 0) return FFA_ERR_MISALIGNED;
   return ffa::launch_paged_decode(*a, static_cast<hipStream_t>(stream));
+}
+
+int ffa_paged_decode_fwd_noalloc(const ffa_paged_decode_args* a, void* stream) {
+  bool empty = false;
+  const int rc = check_decode_args(a, &empty);
+  if (rc != FFA_OK || empty) return rc;
+  return ffa::launch_paged_decode_noalloc(*a, static_cast<hipStream_t>(stream));
 }
 
 size_t ffa_mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,

@@ -27,8 +27,18 @@
 // hold are excluded from the attention like tokens past context_len (a split whose
 // staged ids are all valid pays nothing for this check).
 
+#include <atomic>
+#include <mutex>
+
 #include "ffa_common.h"
 #include "ffa_internal.h"
+
+// Split-K partials of ffa_paged_decode_fwd_noalloc: one array per GPU the library runs
+// on (a device global), held until the process ends. Host code never uses the name
+// itself as memory (on the host it is only a handle): noalloc_scratch() resolves the
+// array's device address per device with hipGetSymbolAddress, and that address is
+// what the kernels are given.
+static __device__ __attribute__((aligned(256))) unsigned char scratch[FFA_NOALLOC_SCRATCH_BYTES];
 
 namespace ffa {
 namespace {
@@ -885,6 +895,50 @@ int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream) {
     launch_decode_tag<F16Tag>(p, softcap, grid, stream);
   }
   return hipGetLastError() == hipSuccess ? FFA_OK : FFA_ERR_LAUNCH;
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array, resolved once per device
+// (with that device current) and kept.
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    return FFA_ERR_NO_DEVICE;
+  }
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) {
+        (void)hipGetLastError();  // leave no error behind for the next call's launch check
+        return FFA_ERR_NO_DEVICE;
+      }
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return FFA_OK;
+}
+
+}  // namespace
+
+int launch_paged_decode_noalloc(const ffa_paged_decode_args& a, hipStream_t stream) {
+  const size_t need = decode_workspace_bytes(a.batch, a.heads_q, a.head_dim, a.max_context_len,
+                                             a.tokens_per_split);
+  if (need > FFA_NOALLOC_SCRATCH_BYTES) return FFA_ERR_SCRATCH_LIMIT;
+  void* ptr = nullptr;
+  const int rc = noalloc_scratch(&ptr);
+  if (rc != FFA_OK) return rc;
+  ffa_paged_decode_args b = a;
+  b.workspace = ptr;
+  b.workspace_bytes = FFA_NOALLOC_SCRATCH_BYTES;
+  return launch_paged_decode(b, stream);
 }
 
 int launch_paged_gather(const ffa_paged_gather_args& a, hipStream_t stream) {

@@ -17,6 +17,8 @@ int32_t decode_tokens_per_split(int32_t tokens_per_split);
 size_t decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
                               int32_t max_context_len, int32_t tokens_per_split);
 int launch_paged_decode(const ffa_paged_decode_args& a, hipStream_t stream);
+// The same launch with the split-K partials in the library's static scratch array.
+int launch_paged_decode_noalloc(const ffa_paged_decode_args& a, hipStream_t stream);
 
 // MLA decode over the compressed latent cache: split kernel + the decode combine kernel.
 int32_t mla_decode_tokens_per_split(int32_t tokens_per_split);

@@ -62,7 +62,9 @@ typedef enum ffa_status {
   FFA_ERR_WORKSPACE = -6,        /* workspace missing or too small */
   FFA_ERR_LAUNCH = -7,           /* hipGetLastError() reported a launch failure */
   FFA_ERR_NO_DEVICE = -8,        /* no usable HIP device / device query failed */
-  FFA_ERR_TOO_LARGE = -9         /* a size exceeds what the kernels index with 32 bits */
+  FFA_ERR_TOO_LARGE = -9,        /* a size exceeds what the kernels index with 32 bits */
+  FFA_ERR_SCRATCH_LIMIT = -10    /* ffa_paged_decode_fwd_noalloc: the call's split-K
+                                    partials exceed FFA_NOALLOC_SCRATCH_BYTES */
 } ffa_status;
 
 typedef enum ffa_dtype {
@@ -252,6 +254,24 @@ int32_t ffa_paged_decode_num_splits(int32_t max_context_len, int32_t tokens_per_
 size_t ffa_paged_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t head_dim,
                                         int32_t max_context_len, int32_t tokens_per_split);
 int ffa_paged_decode_fwd(const ffa_paged_decode_args* args, void* stream);
+
+/*
+ * Allocation-free paged decode. It has no counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, semantics, kernels
+ * and results as ffa_paged_decode_fwd, except that args->workspace and
+ * args->workspace_bytes are ignored: the split-K partials go to a library-owned
+ * device array of FFA_NOALLOC_SCRATCH_BYTES, one per GPU the library runs on, held
+ * until the process ends. A call whose ffa_paged_decode_workspace_bytes() exceeds it
+ * returns FFA_ERR_SCRATCH_LIMIT (fewer, longer splits need less). No memory is
+ * allocated or freed. Every call on one GPU shares that GPU's array and leaves its
+ * partials there: calls that overlap on one GPU (other streams, other threads) race,
+ * so the caller serialises them. Nothing in the array has to start at zero (each
+ * call writes every partial it reads). The first call on a device looks up the
+ * array's address on that device once.
+ */
+#define FFA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int ffa_paged_decode_fwd_noalloc(const ffa_paged_decode_args* args, void* stream);
 
 /*
  * MLA decode over the compressed latent cache (no counterpart in the reference, which
