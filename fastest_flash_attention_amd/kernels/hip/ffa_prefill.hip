@@ -174,7 +174,6 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   // Scores stay in raw units until the exponent: p = exp2(s*c - m*c), with s = q.k and
   // c = scale*log2e, or with softcap s = tanh(q.k * scale / cap) and c = cap*log2e.
   const float c = SOFTCAP ? p.cap_mul : p.score_mul;
-  const float thresh = kRescaleThresh / c;
   const float tanh_mul = 2.0f * kLog2e * p.score_mul;  // softcap: e^{2y} = exp2(s * tanh_mul)
 
   // ---- direct global -> LDS tile loads -------------------------------------------
@@ -293,6 +292,8 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   }
   float m_run = kNegInf;
   float l_run = 0.0f;
+  float negmc = 0.0f;   // -m_run * c (0 while m_run = -inf)
+  float lim = -1.0f;    // chunk exp-sum limit; < 0: no max yet, the first chunk sets it
 
   auto qk = [&](const uint16_t* kl, f32x16 (&sacc)[S::NB]) __attribute__((always_inline)) {
 #pragma unroll
@@ -389,26 +390,44 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
         }
       }
     }
-    float mt = kNegInf;
+    // Running max. CHUNK_CHECK (the interleaved kernels, head_dim <= 128): the max moves
+    // only when a chunk shows it must. The exponents are taken against the current
+    // m_run, and a chunk whose exp sum exceeds kChunkLimit (some p > 2^5, i.e. a score
+    // well above m_run), or any row without a max yet (lim < 0), takes the rare path
+    // below, which sets m_run to the tile's max and rescales O and l, then redoes the
+    // chunk. Every accumulated p is thus <= kChunkLimit, and the common tile spends no
+    // VALU work on its max (-13 % VALU instructions per tile). The other kernels (no
+    // registers to spare for the rare path inside the chunk loop) take the tile's max
+    // first and move m_run when it grows by more than kRescaleThresh.
+    constexpr bool CHUNK_CHECK = IL;
+    if constexpr (!CHUNK_CHECK) {
+      float mt = kNegInf;
 #pragma unroll
-    for (int nb = 0; nb < S::NB; ++nb) {
+      for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[nb][r]);
-    }
-    mt = wave_pair_max(mt);
-    const float m_new = fmaxf(m_run, mt);
-    const bool need = m_new > m_run + thresh;
-    if (__any(need)) {
-      const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
-      m_run = need ? m_new : m_run;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < S::DB; ++db) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[nb][r]);
       }
+      mt = wave_pair_max(mt);
+      const float m_new = fmaxf(m_run, mt);
+      const bool need = m_new > m_run + kRescaleThresh / c;
+      if (__any(need)) {
+        const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
+        m_run = need ? m_new : m_run;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < S::DB; ++db) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        }
+      }
+      negmc = (m_run == kNegInf) ? 0.0f : -m_run * c;
     }
-    const float mc = (m_run == kNegInf) ? 0.0f : m_run * c;
+    bool checked = !CHUNK_CHECK;  // uniform: this tile's max is known, later chunks are safe
+    auto chunk_exp = [&](int nb, int base, float (&pv)[8]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(sacc[nb][base + e], c, negmc));
+      return ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+    };
 #pragma unroll
     for (int cc = 0; cc < S::NC; ++cc) {
       const int nb = cc >> 1;
@@ -434,11 +453,31 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
         }
       }
       float pv[8];
+      float csum = chunk_exp(nb, base, pv);
+      if (!checked && __any(!(csum <= lim))) {
+        checked = true;
+        float mt = kNegInf;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = fast_exp2(fmaf(sacc[nb][base + e], c, -mc));
-        l_run += pv[e];
+        for (int nb2 = 0; nb2 < S::NB; ++nb2) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[nb2][r]);
+        }
+        mt = wave_pair_max(mt);
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = m_new > m_run ? fast_exp2((m_run - m_new) * c) : 1.0f;
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < S::DB; ++db) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        }
+        const bool no_max = m_run == kNegInf;  // every key so far masked
+        negmc = no_max ? 0.0f : -m_run * c;
+        lim = no_max ? -1.0f : kChunkLimit;
+        csum = chunk_exp(nb, base, pv);
       }
+      l_run += csum;
       const u32x4 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]),
                         E::pack2(pv[4], pv[5]), E::pack2(pv[6], pv[7])};
 #pragma unroll

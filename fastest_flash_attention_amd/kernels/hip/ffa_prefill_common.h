@@ -8,6 +8,9 @@ namespace ffa {
 namespace pf {
 
 constexpr float kRescaleThresh = 8.0f;  // log2 units: the running max moves only past this
+// 16-bit kernels: the running max moves when a 16-key chunk's 8 exponentials per lane sum
+// past this (some p > 2^5), so every accumulated p stays <= 2^8.
+constexpr float kChunkLimit = 256.0f;
 
 struct PrefillParams {
   const uint16_t* q;
