@@ -295,10 +295,16 @@ def bench_mla_decode(steps: int, warmup: int):
     lens = torch.full((B,), L, dtype=torch.int32, device="cuda")
     q = torch.randn(B, H, lat + R, generator=gd, device="cuda").to(torch.bfloat16)
     scale = 1.0 / math.sqrt(128 + R)  # the module's 1/sqrt(head_dim + rope_dim)
+    # a serving loop keeps its split-K workspace (caller-owned) across steps
+    from fastest_flash_attention_amd.ops.mla_decode import (_auto_mla_tokens_per_split,
+                                                            mla_decode_workspace_bytes)
+    tps = _auto_mla_tokens_per_split(B, (H + 31) // 32, L)
+    ws = torch.empty(mla_decode_workspace_bytes(B, H, lat, L, tps), dtype=torch.uint8,
+                     device="cuda")
 
     def step():
         ffa.fastest_flash_mla_decode(q, pool, bt, lens, dim_v=lat, scale=scale, return_lse=True,
-                                     max_context_len=L)
+                                     max_context_len=L, tokens_per_split=tps, workspace=ws)
 
     ms_event, ms_wall = time_steps(step, steps, warmup)
     nbytes = B * L * (lat + R) * 2 + B * H * (lat + R) * 2 + B * H * lat * 2 + B * H * 4 + \

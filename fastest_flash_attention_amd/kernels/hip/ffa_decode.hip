@@ -60,7 +60,8 @@ struct DecodeParams {
   float* lse;
   const int32_t* bt;
   const int32_t* lens;
-  float* ws_o;    // [B][Hq][n_splits][DP]
+  float* ws_o;    // [B][Hq][n_splits][DP] fp32 partials (paged decode)
+  const uint16_t* ws_o16;  // [B][Hq][n_splits][DP] 16-bit partials (MLA decode)
   float* ws_lse;  // [B][Hq][n_splits]
   int64_t q_sb, q_sh, o_sb, o_sh, l_sb, l_sh;
   int64_t page_stride;  // Hkv * P * D elements
@@ -386,13 +387,25 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   }
 }
 
+// Partial s of dims d0, d0 + 1 in fp32 (P16: stored in the input's 16-bit type).
+template <typename Tag, bool P16>
+__device__ inline f32x2 load_partial(const DecodeParams& p, int64_t row, int d0) {
+  if constexpr (P16) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p.ws_o16 + row * p.dp + d0);
+    return f32x2{Elem<Tag>::to_f32(static_cast<uint16_t>(w & 0xffffu)),
+                 Elem<Tag>::to_f32(static_cast<uint16_t>(w >> 16))};
+  } else {
+    return *reinterpret_cast<const f32x2*>(p.ws_o + row * p.dp + d0);
+  }
+}
+
 // One workgroup per (sequence, query head): O = sum_s w_s O_s / sum_s w_s with
 // w_s = exp(lse_s - max lse). Lane l owns dims 2l, 2l + 1 of a 128-dim slice, so a
 // split's partial row is one coalesced 512-byte read; splits are walked 8 at a time
 // to keep eight reads in flight per lane. Wave w of the workgroup (blockDim.x / 64
 // waves) takes slices w, w + waves, ...: wide rows (the 512 MLA latent dims) are
 // launched with one wave per slice, so all slices' reads are in flight at once.
-template <typename Tag>
+template <typename Tag, bool P16>
 __global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams p) {
   using E = Elem<Tag>;
   const int bh = blockIdx.x;
@@ -426,14 +439,13 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams 
   for (int d0 = 2 * lane + 128 * wave; d0 < p.D; d0 += 128 * n_waves) {
     f32x2 acc = {0.0f, 0.0f};
     if (mm != kNegInf) {
-      const float* col = p.ws_o + base * p.dp + d0;
       int s = s0;
       for (; s + 8 <= s1; s += 8) {
         f32x2 v[8];
         float w[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          v[u] = *reinterpret_cast<const f32x2*>(col + static_cast<int64_t>(s + u) * p.dp);
+          v[u] = load_partial<Tag, P16>(p, base + s + u, d0);
           w[u] = __expf(lse_row[s + u] - mm);  // exp(-inf) = 0 for empty partials
         }
 #pragma unroll
@@ -443,7 +455,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams 
         }
       }
       for (; s < s1; ++s) {
-        const f32x2 v = *reinterpret_cast<const f32x2*>(col + static_cast<int64_t>(s) * p.dp);
+        const f32x2 v = load_partial<Tag, P16>(p, base + s, d0);
         const float w = __expf(lse_row[s] - mm);
         acc[0] += w * v[0];
         acc[1] += w * v[1];
@@ -496,7 +508,7 @@ struct MlaParams {
   const uint16_t* kv;
   const int32_t* bt;
   const int32_t* lens;
-  float* ws_o;
+  uint16_t* ws_o;  // [B][Hq][n_splits][DV] partials in the input's 16-bit type
   float* ws_lse;
   int64_t q_sb, q_sh;
   int bt_stride;
@@ -521,7 +533,11 @@ __device__ inline int mla_page_of(const MlaParams& p, int tok, int& slot) {
 // rows of a K operand read, and the 4 rows of a transposed V read, over distinct banks.
 __device__ inline int mla_swz(int r) { return (r >> 1) & 7; }
 
-template <typename Tag, int DV>
+// TILE_PAGE: page_size is a multiple of the 32-token tile, so a tile (they start at
+// multiples of 32) never straddles a page: one wave-uniform page lookup per tile, and
+// each load is the tile's base (SGPRs) plus a per-lane 32-bit offset fixed for the whole
+// sweep. Otherwise every row of a tile finds its own page.
+template <typename Tag, int DV, bool TILE_PAGE>
 __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const MlaParams p) {
   using E = Elem<Tag>;
   constexpr int DQK = DV + kMlaRope;
@@ -591,19 +607,57 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   const char* pool = reinterpret_cast<const char*>(p.kv);
   const int n_tiles = (s_end - s_begin + kMlaTile - 1) / kMlaTile;
   // Load j of this lane fills chunk position P = (4j + wave) * 64 + lane of a tile.
+  // Load j of this lane: tile row ld_row(j), byte offset ld_off[j] of its swizzled
+  // chunk inside the tile's rows (rows are contiguous within a page).
+  auto ld_row = [&](int j) { return ((4 * j + wave) * 64 + lane) / CH; };
+  uint32_t ld_off[LPT];
+#pragma unroll
+  for (int j = 0; j < LPT; ++j) {
+    const int pos = (4 * j + wave) * 64 + lane;
+    const int row = pos / CH;
+    const int pc = pos - row * CH;
+    ld_off[j] = static_cast<uint32_t>(row * DQK * 2 + (pc ^ mla_swz(row)) * 16);
+  }
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + wave * 1024);
+  // Page id of tile t (TILE_PAGE): wave-uniform; -1 for an id outside the pool.
+  auto tile_page = [&](int t0) {
+    int slot;
+    const int pg = mla_page_of(p, t0, slot);
+    return __builtin_amdgcn_readfirstlane(bt_lds[pg - pg0]);
+  };
   auto issue = [&](int t, int st) {
     const int t0 = s_begin + t * kMlaTile;
-    uint16_t* dst = ring[st];
-#pragma unroll
-    for (int j = 0; j < LPT; ++j) {
-      const int pos = (4 * j + wave) * 64 + lane;
-      const int row = pos / CH;
-      const int pc = pos - row * CH;
-      const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
+    if constexpr (TILE_PAGE) {
       int slot;
-      const int pg = mla_page_of(p, tok, slot);
-      const int64_t ro = (static_cast<int64_t>(max(bt_lds[pg - pg0], 0)) * p.P + slot) * DQK * 2;
-      load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (4 * j + wave) * 512));
+      mla_page_of(p, t0, slot);
+      const int phys = max(tile_page(t0), 0);
+      const char* tb = pool + (static_cast<int64_t>(phys) * p.P + slot) * DQK * 2;
+      const uint32_t dst = ring_lds + st * TILE * 2;
+      if (t0 + kMlaTile <= s_end) {
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) load_lds16_async(tb, ld_off[j], dst + j * 4096);
+      } else {
+        // last tile of the split: rows past s_end - 1 re-read that row (masked)
+        const int last = s_end - 1 - t0;
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) {
+          const uint32_t back = static_cast<uint32_t>(max(0, ld_row(j) - last) * DQK * 2);
+          load_lds16_async(tb, ld_off[j] - back, dst + j * 4096);
+        }
+      }
+    } else {
+      uint16_t* dst = ring[st];
+#pragma unroll
+      for (int j = 0; j < LPT; ++j) {
+        const int pos = (4 * j + wave) * 64 + lane;
+        const int row = pos / CH;
+        const int pc = pos - row * CH;
+        const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
+        int slot;
+        const int pg = mla_page_of(p, tok, slot);
+        const int64_t ro = (static_cast<int64_t>(max(bt_lds[pg - pg0], 0)) * p.P + slot) * DQK * 2;
+        load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (4 * j + wave) * 512));
+      }
     }
   };
 
@@ -632,26 +686,48 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
 
   auto compute = [&](int t, const uint16_t* tl) {
     const int t0 = s_begin + t * kMlaTile;
-    f32x4 sacc[2];
+    // S^T in four interleaved accumulator chains (key block kb x even / odd k-step),
+    // the K operands read one k-step ahead of their MFMAs: with one wave per SIMD
+    // nothing else hides the LDS and MFMA latencies of a single dependent chain.
+    auto k_at = [&](int ks, int kb) {
+      return *reinterpret_cast<const u32x4*>(tl + ((ks & 1) ? k_rd1 : k_rd0) + (ks >> 1) * 64 +
+                                             kb * 16 * DQK);
+    };
+    f32x4 sp[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      sacc[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sp[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sp[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    u32x4 a_cur[2] = {k_at(0, 0), k_at(0, 1)};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const int off = ((ks & 1) ? k_rd1 : k_rd0) + (ks >> 1) * 64 + kb * 16 * DQK;
-        const u32x4 a = *reinterpret_cast<const u32x4*>(tl + off);
-        sacc[kb] = E::mfma16(a, qreg[ks], sacc[kb]);
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 a_nxt[2];
+      if (ks + 1 < KS) {
+        a_nxt[0] = k_at(ks + 1, 0);
+        a_nxt[1] = k_at(ks + 1, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) sp[kb][ks & 1] = E::mfma16(a_cur[kb], qreg[ks], sp[kb][ks & 1]);
+      if (ks + 1 < KS) {
+        a_cur[0] = a_nxt[0];
+        a_cur[1] = a_nxt[1];
       }
     }
+    f32x4 sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) sacc[kb] = sp[kb][0] + sp[kb][1];
     // S^T lane layout: keys 16 kb + 4 g4 + j of head c16
+    const bool tile_ok = !TILE_PAGE || !any_bad || tile_page(t0) >= 0;  // uniform
     float mt = kNegInf;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tok = t0 + 16 * kb + 4 * g4 + j;
-        bool live = tok < s_end;
-        if (any_bad && live) {
+        bool live = tok < s_end && tile_ok;
+        if (!TILE_PAGE && any_bad && live) {
           int slot;
           live = bt_lds[mla_page_of(p, tok, slot) - pg0] >= 0;
         }
@@ -698,20 +774,30 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
     }
   };
 
-  issue(0, 0);
-  if (n_tiles > 1) issue(1, 1);
+  // kMlaStages-deep ring: tiles t + 1 .. t + kMlaStages - 1 stay in flight while tile t
+  // is computed (the vmcnt counter retires loads in order, so waiting until at most
+  // `ahead` tiles' loads remain leaves tile t complete).
+  static_assert(kMlaStages >= 2 && kMlaStages <= 4 && (kMlaStages - 1) * LPT < 64, "vmcnt range");
+  for (int t = 0; t < kMlaStages && t < n_tiles; ++t) issue(t, t);
+  int st = 0;
   for (int t = 0; t < n_tiles; ++t) {
-    if (t + 1 < n_tiles) {
+    const int ahead = min(kMlaStages - 1, n_tiles - 1 - t);
+    if (ahead >= 3) {
+      wait_vmcnt<3 * LPT>();
+    } else if (ahead == 2) {
+      wait_vmcnt<2 * LPT>();
+    } else if (ahead == 1) {
       wait_vmcnt<LPT>();
     } else {
       wait_vmcnt0();
     }
     __syncthreads();  // tile t is in LDS
-    compute(t, ring[t & 1]);
-    if (t + 2 < n_tiles) {
-      __syncthreads();  // every wave is done with stage t & 1
-      issue(t + 2, t & 1);
+    compute(t, ring[st]);
+    if (t + kMlaStages < n_tiles) {
+      __syncthreads();  // every wave is done with stage st
+      issue(t + kMlaStages, st);
     }
+    st = st + 1 == kMlaStages ? 0 : st + 1;
   }
 
   // Partial of this split: O^T lane layout dims 16 db + 4 g4 + j (of this wave's
@@ -721,11 +807,15 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   if (!head_live) return;
   const int64_t row = (static_cast<int64_t>(b) * p.Hq + head) * p.n_splits + split;
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  float* wo = p.ws_o + row * DV + dq * DW + 4 * g4;
+  // A normalised partial is a convex combination of latent rows, so it fits the
+  // input's 16-bit type: half the partial traffic of fp32 (both the write here and the
+  // combine's read).
+  uint16_t* wo = p.ws_o + row * DV + dq * DW + 4 * g4;
 #pragma unroll
   for (int db = 0; db < DBW; ++db) {
-    const f32x4 v = {oacc[db][0] * inv, oacc[db][1] * inv, oacc[db][2] * inv, oacc[db][3] * inv};
-    *reinterpret_cast<f32x4*>(wo + 16 * db) = v;
+    const u32x2 v = {E::pack2(oacc[db][0] * inv, oacc[db][1] * inv),
+                     E::pack2(oacc[db][2] * inv, oacc[db][3] * inv)};
+    *reinterpret_cast<u32x2*>(wo + 16 * db) = v;
   }
   if (dq == 0 && g4 == 0) {
     p.ws_lse[row] = l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : kNegInf;
@@ -814,7 +904,7 @@ void launch_decode_tag(DecodeParams& p, bool softcap, dim3 grid, hipStream_t s) 
     p.dp = 256;
     launch_decode_dp<Tag, 256>(p, softcap, grid, s);
   }
-  hipLaunchKernelGGL((decode_combine_kernel<Tag>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
+  hipLaunchKernelGGL((decode_combine_kernel<Tag, false>), dim3(p.B * p.Hq), dim3(64), 0, s, p);
 }
 
 int dp_of(int d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : d <= 192 ? 192 : 256; }
@@ -1037,7 +1127,8 @@ size_t mla_decode_workspace_bytes(int32_t batch, int32_t heads_q, int32_t dim_v,
                                   int32_t max_context_len, int32_t tokens_per_split) {
   const size_t ns = static_cast<size_t>(mla_decode_num_splits(max_context_len, tokens_per_split));
   const size_t rows = static_cast<size_t>(batch) * heads_q * ns;
-  return rows * (static_cast<size_t>(dim_v) + 1) * sizeof(float);
+  // 16-bit O partials, then fp32 lse partials (rows * dim_v * 2 keeps them 16-byte aligned)
+  return rows * (static_cast<size_t>(dim_v) * 2 + sizeof(float));
 }
 
 namespace {
@@ -1045,13 +1136,22 @@ namespace {
 template <typename Tag>
 void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3 grid,
                     hipStream_t s) {
+  const bool tile_page = mp.P % kMlaTile == 0;
   if (dim_v == 512) {
-    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512>), grid, dim3(kMlaThreads), 0, s, mp);
+    if (tile_page) {
+      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512, true>), grid, dim3(kMlaThreads), 0, s, mp);
+    } else {
+      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512, false>), grid, dim3(kMlaThreads), 0, s, mp);
+    }
   } else {
-    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256>), grid, dim3(kMlaThreads), 0, s, mp);
+    if (tile_page) {
+      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256, true>), grid, dim3(kMlaThreads), 0, s, mp);
+    } else {
+      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256, false>), grid, dim3(kMlaThreads), 0, s, mp);
+    }
   }
   // one wave per 128-dim slice of the dim_v = 256 or 512 latent output dims
-  hipLaunchKernelGGL((decode_combine_kernel<Tag>), dim3(cp.B * cp.Hq), dim3(dim_v / 2), 0, s, cp);
+  hipLaunchKernelGGL((decode_combine_kernel<Tag, true>), dim3(cp.B * cp.Hq), dim3(dim_v / 2), 0, s, cp);
 }
 
 }  // namespace
@@ -1075,15 +1175,15 @@ int launch_mla_decode(const ffa_mla_decode_args& a, hipStream_t stream) {
   mp.max_len = a.max_context_len;
   mp.score_mul = a.scale * kLog2e;
   const size_t rows = static_cast<size_t>(a.batch) * a.heads_q * mp.n_splits;
-  mp.ws_o = static_cast<float*>(a.workspace);
-  mp.ws_lse = mp.ws_o + rows * a.dim_v;
+  mp.ws_o = static_cast<uint16_t*>(a.workspace);
+  mp.ws_lse = reinterpret_cast<float*>(mp.ws_o + rows * a.dim_v);
 
   // the split-K merge is the paged-decode combine kernel over dim_v output dims
   DecodeParams cp{};
   cp.o = static_cast<uint16_t*>(a.o);
   cp.lse = a.lse;
   cp.lens = a.context_lens;
-  cp.ws_o = mp.ws_o;
+  cp.ws_o16 = mp.ws_o;
   cp.ws_lse = mp.ws_lse;
   cp.o_sb = a.o_stride[0];
   cp.o_sh = a.o_stride[1];

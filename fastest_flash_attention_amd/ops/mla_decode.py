@@ -32,11 +32,12 @@ MLA_LATENT_DIMS = (256, 512)
 
 
 def _auto_mla_tokens_per_split(batch: int, head_groups: int, max_len: int) -> int:
-    """Largest split (<= 1024 tokens, >= 64) that still gives >= 512 workgroups (two per
-    CU on 256 CUs); fewer splits keep the fp32 partials small. On MI355X at batch 32,
-    context 4096 this picks 256 tokens (43.9 us per step; 512 tokens: 46.7 us)."""
+    """Largest split (<= 1024 tokens, >= 64) that still gives >= 256 workgroups (one per
+    CU on 256 CUs); fewer splits mean fewer partials to write and merge. On MI355X at
+    batch 32, context 4096 this picks 512 tokens (34.4-35.8 us per step; 256 tokens with
+    two workgroups per CU: 38.6 us; 1024 tokens, 128 workgroups: about 51 us)."""
     tps = 1024
-    while tps > 64 and batch * head_groups * max(1, math.ceil(max_len / tps)) < 512:
+    while tps > 64 and batch * head_groups * max(1, math.ceil(max_len / tps)) < 256:
         tps //= 2
     return tps
 

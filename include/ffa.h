@@ -290,7 +290,9 @@ int ffa_paged_decode_fwd_noalloc(const ffa_paged_decode_args* args, void* stream
  * kv_pages are 16-byte aligned, q's strides multiples of 8 (FFA_ERR_MISALIGNED).
  * tokens_per_split (0: library default 512) is rounded up to a multiple of 32 and
  * capped at 1024, and ceil(max_context_len / tokens_per_split) must not exceed 65535
- * (FFA_ERR_TOO_LARGE); partials go to the workspace as in ffa_paged_decode_fwd.
+ * (FFA_ERR_TOO_LARGE); split-K partials go to the workspace: normalised O partials in
+ * the input's 16-bit type (a convex combination of latent rows is representable there)
+ * and one fp32 lse per (sequence, head, split), merged as in ffa_paged_decode_fwd.
  */
 typedef struct ffa_mla_decode_args {
   const void* q;

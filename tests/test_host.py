@@ -246,11 +246,12 @@ def test_workspace_sizing(lib):
     assert lib.ffa_paged_decode_num_splits(100, 40) == 3  # 40 rounds up to 48 (16-token tiles)
     assert lib.ffa_paged_decode_workspace_bytes(64, 32, 128, 32768, 512) == 64 * 32 * 64 * 129 * 4
     assert lib.ffa_paged_decode_workspace_bytes(2, 4, 100, 100, 64) == 2 * 4 * 2 * 129 * 4
-    # MLA: 32-token tiles, default split 512, capped at 1024; dim_v-wide partials
-    assert lib.ffa_mla_decode_workspace_bytes(32, 32, 512, 4096, 512) == 32 * 32 * 8 * 513 * 4
-    assert lib.ffa_mla_decode_workspace_bytes(2, 8, 256, 1000, 0) == 2 * 8 * 2 * 257 * 4
-    assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 5000, 4096) == 5 * 513 * 4
-    assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 100, 40) == 2 * 513 * 4  # 40 -> 64
+    # MLA: 32-token tiles, default split 512, capped at 1024; dim_v-wide 16-bit O partials
+    # plus one fp32 lse per (sequence, head, split)
+    assert lib.ffa_mla_decode_workspace_bytes(32, 32, 512, 4096, 512) == 32 * 32 * 8 * (1024 + 4)
+    assert lib.ffa_mla_decode_workspace_bytes(2, 8, 256, 1000, 0) == 2 * 8 * 2 * (512 + 4)
+    assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 5000, 4096) == 5 * (1024 + 4)
+    assert lib.ffa_mla_decode_workspace_bytes(1, 1, 512, 100, 40) == 2 * (1024 + 4)  # 40 -> 64
     # backward: lse2 and D_i, fp32, rows padded to 128 per (batch, q head)
     assert lib.ffa_attn_bwd_workspace_bytes(2, 3, 100) == 2 * 2 * 3 * 128 * 4
     assert lib.ffa_attn_bwd_workspace_bytes(1, 1, 256) == 2 * 256 * 4
