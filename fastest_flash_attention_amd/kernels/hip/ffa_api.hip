@@ -267,8 +267,8 @@ size_t ffa_attn_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seql
 
 int ffa_attn_bwd(const ffa_attn_bwd_args* a, void* stream) {
   if (a == nullptr) return FFA_ERR_INVALID_ARG;
-  if (!valid_dtype(a->dtype)) return FFA_ERR_UNSUPPORTED_DTYPE;
-  if (a->head_dim < 1 || a->head_dim > 128) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  if (!valid_dtype(a->dtype) && a->dtype != FFA_DTYPE_FP32) return FFA_ERR_UNSUPPORTED_DTYPE;
+  if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
   if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->seqlen_q < 0 || a->seqlen_kv < 0) {
     return FFA_ERR_INVALID_ARG;
   }

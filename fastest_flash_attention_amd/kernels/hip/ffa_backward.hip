@@ -35,6 +35,8 @@
 // fp32. Inputs are 16-byte aligned with head_dim % 8 == 0 (the host pads otherwise);
 // head_dim up to 128.
 
+#include <type_traits>
+
 #include "ffa_common.h"
 #include "ffa_grid.h"
 #include "ffa_internal.h"
@@ -97,9 +99,15 @@ __device__ inline void bwd_item(int bid, int n_t, int g, int remap, int& u, int&
 // one row parity for 128-byte rows); ds_read_b64_tr_b16 (rows r0..r0+3, r0 % 4 == 0,
 // 4 consecutive chunks) needs swz(r) >> 2 distinct over those 4 rows (128-byte rows:
 // rows of one parity distinct). swz(r + 16) == swz(r) for both widths.
+// Rows of 256 or 512 bytes (DP = 128, 256) start in the same bank group: a 4-bit
+// swizzle over the low chunk bits; rows of 128 or 384 bytes (DP = 64, 192) alternate
+// between two half bank rows: a 3-bit swizzle injective over rows of one parity.
+template <int DP>
+constexpr int kSwBits = (DP == 64 || DP == 192) ? 3 : 4;
+
 template <int DP>
 __device__ inline int bswz(int r) {
-  if constexpr (DP == 128) {
+  if constexpr (kSwBits<DP> == 4) {
     return ((r & 3) << 2) | ((r >> 2) & 3);
   } else {
     const int s = (r >> 1) & 7;
@@ -145,10 +153,12 @@ __device__ inline void store_rows(uint16_t* row, const f32x16 (&acc)[BShape<DP>:
   }
 }
 
-// Element offsets inside a swizzled [rows, DP] tile are row * DP | chunk << 3 | elem,
-// with disjoint bit fields, so moving to chunk c ^ m is an XOR of the offset with
-// m << 3: one base offset per lane serves every k-step and dim block (the per-step
-// offsets are not held in registers).
+// Element offsets inside a swizzled [rows, DP] tile are row * DP + chunk' * 8 + elem,
+// chunk' = chunk ^ bswz(row), which only touches the low SW = kSwBits chunk bits; row * DP
+// is a multiple of 8 * 2^SW for every DP. So moving from one chunk to another is an XOR
+// inside the low SW + 3 offset bits plus an addition above them: one base offset per
+// lane serves every k-step and dim block (the per-step offsets are not held in
+// registers).
 //
 // Row-wise A operand of k-step ks: tile row l32, chunk 2 ks + g.
 template <int DP>
@@ -156,7 +166,11 @@ __device__ inline int row_rd0(int lane) {
   const int l32 = lane & 31;
   return l32 * DP + ((((lane >> 5)) ^ bswz<DP>(l32)) << 3);
 }
-__device__ inline int row_rd(int base, int ks) { return base ^ (ks << 4); }
+template <int DP>
+__device__ inline int row_rd(int base, int ks) {
+  constexpr int SW = kSwBits<DP>;
+  return (base ^ ((ks & ((1 << (SW - 1)) - 1)) << 4)) + ((ks >> (SW - 1)) << (SW + 3));
+}
 
 // The two ds_read_b64_tr_b16 reads (rows 4g + 0..3 and 8 + 4g + 0..3 of a 16-row chunk;
 // dims colw .. colw + 3 of a 32-dim block) that form the A operand [32 dims x 16 rows]
@@ -179,18 +193,48 @@ __device__ inline int opaque(int x) {
   return x;
 }
 
+template <int DP>
+__device__ inline int tr_at(int base, int db) {
+  constexpr int SW = kSwBits<DP>;
+  return (base ^ ((db & ((1 << (SW - 2)) - 1)) << 5)) + ((db >> (SW - 2)) << (SW + 3));
+}
+
+template <int DP>
 __device__ inline u32x4 tr_operand(const uint16_t* tile, int lo, int hi, int db) {
-  const u32x2 a = lds_read_tr16(tile + (lo ^ (db << 5)));
-  const u32x2 b = lds_read_tr16(tile + (hi ^ (db << 5)));
+  const u32x2 a = lds_read_tr16(tile + tr_at<DP>(lo, db));
+  const u32x2 b = lds_read_tr16(tile + tr_at<DP>(hi, db));
   return u32x4{a[0], a[1], b[0], b[1]};
 }
 
 // ---------------------------------------------------------------------------------
 // 1. lse2 and D_i. 32 rows per workgroup, 8 lanes per row.
 // ---------------------------------------------------------------------------------
+// 8 elements of O or dO starting at `row + 8 c` as fp32 (16-bit tags, or F32Tag).
+struct F32Tag {};
+template <typename Tag>
+__device__ inline void load8_f32(const uint16_t* row, int c, float (&x)[8]) {
+  if constexpr (std::is_same_v<Tag, F32Tag>) {
+    const float* r = reinterpret_cast<const float*>(row) + 8 * c;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(r);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(r + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = a[e];
+      x[4 + e] = b[e];
+    }
+  } else {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(row + 8 * c);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      x[2 * w] = Elem<Tag>::to_f32(static_cast<uint16_t>(v[w] & 0xffffu));
+      x[2 * w + 1] = Elem<Tag>::to_f32(static_cast<uint16_t>(v[w] >> 16));
+    }
+  }
+}
+
 template <typename Tag>
 __global__ __launch_bounds__(kThreads) void bwd_pre_kernel(const BwdParams p) {
-  using E = Elem<Tag>;
+  constexpr int EB = std::is_same_v<Tag, F32Tag> ? 2 : 1;  // element size in 16-bit units
   const int tid = threadIdx.x;
   const int part = tid & 7;
   const int64_t rg = static_cast<int64_t>(blockIdx.x) * 32 + (tid >> 3);  // < B*Hq*sq_pad
@@ -200,18 +244,16 @@ __global__ __launch_bounds__(kThreads) void bwd_pre_kernel(const BwdParams p) {
   const int h = bh - b * p.Hq;
   float acc = 0.0f;
   if (s < p.Sq) {
-    const uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(s) * p.o_ss;
-    const uint16_t* drow = p.dout + b * p.do_sb + h * p.do_sh + static_cast<int64_t>(s) * p.do_ss;
+    const uint16_t* orow =
+        p.o + EB * (b * p.o_sb + h * p.o_sh + static_cast<int64_t>(s) * p.o_ss);
+    const uint16_t* drow =
+        p.dout + EB * (b * p.do_sb + h * p.do_sh + static_cast<int64_t>(s) * p.do_ss);
     for (int c = part; c < (p.D >> 3); c += 8) {
-      const u32x4 ov = *reinterpret_cast<const u32x4*>(orow + 8 * c);
-      const u32x4 dv = *reinterpret_cast<const u32x4*>(drow + 8 * c);
+      float ov[8], dv[8];
+      load8_f32<Tag>(orow, c, ov);
+      load8_f32<Tag>(drow, c, dv);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        acc = fmaf(E::to_f32(static_cast<uint16_t>(ov[w] & 0xffffu)),
-                   E::to_f32(static_cast<uint16_t>(dv[w] & 0xffffu)), acc);
-        acc = fmaf(E::to_f32(static_cast<uint16_t>(ov[w] >> 16)),
-                   E::to_f32(static_cast<uint16_t>(dv[w] >> 16)), acc);
-      }
+      for (int e = 0; e < 8; ++e) acc = fmaf(ov[e], dv[e], acc);
     }
   }
   acc += __shfl_xor(acc, 1);
@@ -233,8 +275,13 @@ __global__ __launch_bounds__(kThreads) void bwd_pre_kernel(const BwdParams p) {
 // ---------------------------------------------------------------------------------
 // 2. dK, dV: keys stationary.
 // ---------------------------------------------------------------------------------
+// Two workgroups per CU up to head_dim 128; wider rows keep their dK / dV (or dQ)
+// accumulators in AGPRs at one workgroup per CU.
+template <int DP>
+constexpr int kBwdMinBlocks = DP <= 128 ? 2 : 1;
+
 template <typename Tag, int DP, bool SOFTCAP>
-__global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p) {
+__global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(const BwdParams p) {
   using S = BShape<DP>;
   using E = Elem<Tag>;
   constexpr int TILE = kDkvRows * DP;
@@ -409,16 +456,16 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
       dpacc[r] = 0.0f;
     }
     // operands one k-step ahead of the MFMAs that consume them
-    u32x4 aq = *reinterpret_cast<const u32x4*>(ql + row_rd(a_rd, 0));
-    u32x4 ad = *reinterpret_cast<const u32x4*>(dl + row_rd(a_rd, 0));
-    u32x4 bv = *reinterpret_cast<const u32x4*>(vw + row_rd(a_rd, 0));
+    u32x4 aq = *reinterpret_cast<const u32x4*>(ql + row_rd<DP>(a_rd, 0));
+    u32x4 ad = *reinterpret_cast<const u32x4*>(dl + row_rd<DP>(a_rd, 0));
+    u32x4 bv = *reinterpret_cast<const u32x4*>(vw + row_rd<DP>(a_rd, 0));
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
       u32x4 aq_n, ad_n, bv_n;
       if (ks + 1 < S::KS) {
-        aq_n = *reinterpret_cast<const u32x4*>(ql + row_rd(a_rd, ks + 1));
-        ad_n = *reinterpret_cast<const u32x4*>(dl + row_rd(a_rd, ks + 1));
-        bv_n = *reinterpret_cast<const u32x4*>(vw + row_rd(a_rd, ks + 1));
+        aq_n = *reinterpret_cast<const u32x4*>(ql + row_rd<DP>(a_rd, ks + 1));
+        ad_n = *reinterpret_cast<const u32x4*>(dl + row_rd<DP>(a_rd, ks + 1));
+        bv_n = *reinterpret_cast<const u32x4*>(vw + row_rd<DP>(a_rd, ks + 1));
       }
       __builtin_amdgcn_sched_barrier(0);
       sacc = E::mfma32(aq, kreg[ks], sacc);
@@ -471,8 +518,8 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
                         E::pack2(dsv[e0 + 4], dsv[e0 + 5]), E::pack2(dsv[e0 + 6], dsv[e0 + 7])};
 #pragma unroll
       for (int db = 0; db < S::DB; ++db) {
-        const u32x4 ado = tr_operand(dl + 16 * cc * DP, t_lo, t_hi, db);
-        const u32x4 aq = tr_operand(ql + 16 * cc * DP, t_lo, t_hi, db);
+        const u32x4 ado = tr_operand<DP>(dl + 16 * cc * DP, t_lo, t_hi, db);
+        const u32x4 aq = tr_operand<DP>(ql + 16 * cc * DP, t_lo, t_hi, db);
         dvacc[db] = E::mfma32(ado, bp, dvacc[db]);
         dkacc[db] = E::mfma32(aq, bs, dkacc[db]);
       }
@@ -491,7 +538,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dkdv_kernel(const BwdParams p
 // 3. dQ: queries stationary.
 // ---------------------------------------------------------------------------------
 template <typename Tag, int DP, bool SOFTCAP>
-__global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(const BwdParams p) {
+__global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(const BwdParams p) {
   using S = BShape<DP>;
   using E = Elem<Tag>;
   constexpr int BN = kKeyTile;
@@ -622,8 +669,8 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(const BwdParams p) 
     for (int ks = 0; ks < S::KS; ++ks) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        const u32x4 ak = *reinterpret_cast<const u32x4*>(kl + row_rd(a_rd, ks) + nb * 32 * DP);
-        const u32x4 av = *reinterpret_cast<const u32x4*>(vl + row_rd(a_rd, ks) + nb * 32 * DP);
+        const u32x4 ak = *reinterpret_cast<const u32x4*>(kl + row_rd<DP>(a_rd, ks) + nb * 32 * DP);
+        const u32x4 av = *reinterpret_cast<const u32x4*>(vl + row_rd<DP>(a_rd, ks) + nb * 32 * DP);
         sacc[nb] = E::mfma32(ak, qreg[ks], sacc[nb]);
         dpacc[nb] = E::mfma32(av, doreg[ks], dpacc[nb]);
       }
@@ -669,7 +716,7 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(const BwdParams p) 
                         E::pack2(dsv[nb][e0 + 6], dsv[nb][e0 + 7])};
 #pragma unroll
       for (int db = 0; db < S::DB; ++db) {
-        const u32x4 ak = tr_operand(kl + 16 * cc * DP, t_lo, t_hi, db);
+        const u32x4 ak = tr_operand<DP>(kl + 16 * cc * DP, t_lo, t_hi, db);
         dqacc[db] = E::mfma32(ak, bs, dqacc[db]);
       }
     }
@@ -678,6 +725,244 @@ __global__ __launch_bounds__(kThreads, 2) void bwd_dq_kernel(const BwdParams p) 
   if (wave_live && qrow < p.Sq) {
     store_rows<Tag, DP>(p.dq + b * p.dq_sb + h * p.dq_sh + static_cast<int64_t>(qrow) * p.dq_ss,
                         dqacc, p.scale, D, g);
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// fp32 inputs: the reference computes them in fp32 (cpu_reference.py:319-427), so they
+// run on fp32 FMAs. A workgroup (256 threads) owns 32 keys (dK / dV) or 32 query rows
+// (dQ) and sweeps 32-row tiles of the other side through LDS, rows padded by one float
+// so the 32 rows read together at one dim fall in 32 distinct banks. Per tile, thread t
+// computes the scores of key (or row) t % 32 against rows t / 32 + 8 i (i < 4), and
+// P / dS go through LDS to the accumulation, where thread t owns dims t / 32 + 8 j of
+// key (or row) t % 32.
+// ---------------------------------------------------------------------------------
+constexpr int kF32T = 32;  // keys or rows per workgroup, rows per tile
+
+// P and dS of the pairs (row rb + 8 i of the row tile, key kk of the key tile) from the
+// two fp32 tiles in LDS; `row_ok(i)` / `key_of` give the mask inputs.
+template <bool SOFTCAP, int PITCH>
+__device__ inline void f32_pairs(const BwdParams& p, const float* rowt_q, const float* rowt_do,
+                                 const float* keyt_k, const float* keyt_v, const float* stats,
+                                 int kk, int rb, int q0_abs, int q_valid, int key, bool key_ok,
+                                 float (&pv)[4], float (&dsv)[4]) {
+  float sc[4] = {0.f, 0.f, 0.f, 0.f};
+  float dp[4] = {0.f, 0.f, 0.f, 0.f};
+  const float* kr = keyt_k + kk * PITCH;
+  const float* vr = keyt_v + kk * PITCH;
+  for (int d = 0; d < p.D; ++d) {
+    const float kv = kr[d];
+    const float vv = vr[d];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = fmaf(rowt_q[(rb + 8 * i) * PITCH + d], kv, sc[i]);
+      dp[i] = fmaf(rowt_do[(rb + 8 * i) * PITCH + d], vv, dp[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = rb + 8 * i;
+    const int qa = q0_abs + r;
+    const bool ok = key_ok && r < q_valid && (!p.causal || key <= qa) &&
+                    (p.window <= 0 || key >= qa - p.window + 1);
+    const float l2 = stats[r];
+    const float di = stats[kF32T + r];
+    float pr, ds;
+    if constexpr (SOFTCAP) {
+      const float t = tanh_fast(sc[i] * p.tanh_mul);
+      pr = fast_exp2(fmaf(t, p.cap_mul, -l2));
+      ds = pr * (dp[i] - di) * fmaf(-t, t, 1.0f);
+    } else {
+      pr = fast_exp2(fmaf(sc[i], p.score_mul, -l2));
+      ds = pr * (dp[i] - di);
+    }
+    pv[i] = ok ? pr : 0.0f;
+    dsv[i] = ok ? ds : 0.0f;
+  }
+}
+
+// rows [r0, r0 + 32) of a [*, D] fp32 tensor (row stride ss elements, rows past `last`
+// clamped to it) into a padded LDS tile; dims >= D are not read
+template <int PITCH>
+__device__ inline void f32_tile(float* t, const float* base, int64_t ss, int r0, int last, int D) {
+  for (int idx = threadIdx.x; idx < kF32T * D; idx += kThreads) {
+    const int r = idx / D;
+    const int d = idx - r * D;
+    t[r * PITCH + d] = base[static_cast<int64_t>(min(r0 + r, last)) * ss + d];
+  }
+}
+
+template <int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads) void bwd_f32_dkdv_kernel(const BwdParams p) {
+  constexpr int PITCH = DP + 1;
+  constexpr int NJ = DP / 8;
+  __shared__ float kt[kF32T * PITCH], vt[kF32T * PITCH], qt[kF32T * PITCH], dt[kF32T * PITCH];
+  __shared__ float pt[kF32T][kF32T + 1], st[kF32T][kF32T + 1];
+  __shared__ float stats[2 * kF32T];
+  const int tid = threadIdx.x;
+  const int kk = tid & 31;
+  const int rb = tid >> 5;
+  const int n_kt = (p.Skv + kF32T - 1) / kF32T;
+  const int bh = blockIdx.x / n_kt;
+  const int k0 = (blockIdx.x - bh * n_kt) * kF32T;
+  const int b = bh / p.Hkv;
+  const int hk = bh - b * p.Hkv;
+  const int D = p.D;
+  const float* q = reinterpret_cast<const float*>(p.q);
+  const float* k = reinterpret_cast<const float*>(p.k);
+  const float* v = reinterpret_cast<const float*>(p.v);
+  const float* dout = reinterpret_cast<const float*>(p.dout);
+  f32_tile<PITCH>(kt, k + b * p.k_sb + hk * p.k_sh, p.k_ss, k0, p.Skv - 1, D);
+  f32_tile<PITCH>(vt, v + b * p.v_sb + hk * p.v_sh, p.v_ss, k0, p.Skv - 1, D);
+  const int key = k0 + kk;
+  const int k_last = min(k0 + kF32T, p.Skv) - 1;
+  // q rows that can see a key of [k0, k_last]
+  const int q_lo = p.causal ? max(0, k0 - p.q_offset) : 0;
+  const int q_hi = p.window > 0 ? static_cast<int>(min<int64_t>(
+                                      p.Sq, static_cast<int64_t>(k_last) + p.window - p.q_offset))
+                                : p.Sq;
+  float dk[NJ], dv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    dk[j] = 0.0f;
+    dv[j] = 0.0f;
+  }
+  for (int r = 0; r < p.ratio; ++r) {
+    const int hq = hk * p.ratio + r;
+    const float* qb = q + b * p.q_sb + hq * p.q_sh;
+    const float* db = dout + b * p.do_sb + hq * p.do_sh;
+    const int64_t ws = (static_cast<int64_t>(b) * p.Hq + hq) * p.sq_pad;
+    for (int q0 = q_lo / kF32T * kF32T; q0 < q_hi; q0 += kF32T) {
+      __syncthreads();  // the previous tile's reads are done
+      f32_tile<PITCH>(qt, qb, p.q_ss, q0, p.Sq - 1, D);
+      f32_tile<PITCH>(dt, db, p.do_ss, q0, p.Sq - 1, D);
+      if (tid < 2 * kF32T) {
+        stats[tid] = (tid < kF32T ? p.lse2 : p.di)[ws + q0 + (tid & (kF32T - 1))];
+      }
+      __syncthreads();
+      float pv[4], dsv[4];
+      f32_pairs<SOFTCAP, PITCH>(p, qt, dt, kt, vt, stats, kk, rb, p.q_offset + q0, p.Sq - q0, key,
+                                key < p.Skv, pv, dsv);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pt[rb + 8 * i][kk] = pv[i];
+        st[rb + 8 * i][kk] = dsv[i];
+      }
+      __syncthreads();
+      // dV[key, d] += P[row, key] dO[row, d];  dK[key, d] += dS[row, key] Q[row, d]
+      for (int row = 0; row < kF32T; ++row) {
+        const float pr = pt[row][kk];
+        const float ds = st[row][kk];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          const int d = rb + 8 * j;
+          if (d < D) {
+            dv[j] = fmaf(pr, dt[row * PITCH + d], dv[j]);
+            dk[j] = fmaf(ds, qt[row * PITCH + d], dk[j]);
+          }
+        }
+      }
+    }
+  }
+  if (key < p.Skv) {
+    float* dkr = reinterpret_cast<float*>(p.dk) + b * p.dk_sb + hk * p.dk_sh +
+                 static_cast<int64_t>(key) * p.dk_ss;
+    float* dvr = reinterpret_cast<float*>(p.dv) + b * p.dv_sb + hk * p.dv_sh +
+                 static_cast<int64_t>(key) * p.dv_ss;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int d = rb + 8 * j;
+      if (d < D) {
+        dkr[d] = dk[j] * p.scale;
+        dvr[d] = dv[j];
+      }
+    }
+  }
+}
+
+template <int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads) void bwd_f32_dq_kernel(const BwdParams p) {
+  constexpr int PITCH = DP + 1;
+  constexpr int NJ = DP / 8;
+  __shared__ float qt[kF32T * PITCH], dt[kF32T * PITCH], kt[kF32T * PITCH], vt[kF32T * PITCH];
+  __shared__ float st[kF32T][kF32T + 1];
+  __shared__ float stats[2 * kF32T];
+  const int tid = threadIdx.x;
+  const int kk = tid & 31;  // key of the pair phase, row of the accumulation phase
+  const int rb = tid >> 5;
+  const int n_qt = (p.Sq + kF32T - 1) / kF32T;
+  const int bh = blockIdx.x / n_qt;
+  const int q0 = (blockIdx.x - bh * n_qt) * kF32T;
+  const int b = bh / p.Hq;
+  const int h = bh - b * p.Hq;
+  const int hk = h / p.ratio;
+  const int D = p.D;
+  f32_tile<PITCH>(qt, reinterpret_cast<const float*>(p.q) + b * p.q_sb + h * p.q_sh, p.q_ss, q0,
+                  p.Sq - 1, D);
+  f32_tile<PITCH>(dt, reinterpret_cast<const float*>(p.dout) + b * p.do_sb + h * p.do_sh,
+                  p.do_ss, q0, p.Sq - 1, D);
+  const int64_t ws = static_cast<int64_t>(bh) * p.sq_pad;
+  if (tid < 2 * kF32T) stats[tid] = (tid < kF32T ? p.lse2 : p.di)[ws + q0 + (tid & (kF32T - 1))];
+  const float* kb = reinterpret_cast<const float*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const float* vb = reinterpret_cast<const float*>(p.v) + b * p.v_sb + hk * p.v_sh;
+  const int q0_abs = p.q_offset + q0;
+  const int ql_abs = p.q_offset + min(q0 + kF32T, p.Sq) - 1;
+  const int kv_lo = p.window > 0 ? max(0, q0_abs - p.window + 1) : 0;
+  const int kv_hi = p.causal ? min(p.Skv, ql_abs + 1) : p.Skv;
+  float dq[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) dq[j] = 0.0f;
+  for (int k0 = kv_lo / kF32T * kF32T; k0 < kv_hi; k0 += kF32T) {
+    __syncthreads();  // the previous tile's reads are done
+    f32_tile<PITCH>(kt, kb, p.k_ss, k0, p.Skv - 1, D);
+    f32_tile<PITCH>(vt, vb, p.v_ss, k0, p.Skv - 1, D);
+    __syncthreads();
+    float pv[4], dsv[4];
+    const int key = k0 + kk;
+    f32_pairs<SOFTCAP, PITCH>(p, qt, dt, kt, vt, stats, kk, rb, q0_abs, p.Sq - q0, key,
+                              key < p.Skv, pv, dsv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st[rb + 8 * i][kk] = dsv[i];
+    __syncthreads();
+    // dQ[row, d] += dS[row, key] K[key, d]  (row = kk here)
+    for (int kx = 0; kx < kF32T; ++kx) {
+      const float ds = st[kk][kx];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int d = rb + 8 * j;
+        if (d < D) dq[j] = fmaf(ds, kt[kx * PITCH + d], dq[j]);
+      }
+    }
+  }
+  if (q0 + kk < p.Sq) {
+    float* dqr = reinterpret_cast<float*>(p.dq) + b * p.dq_sb + h * p.dq_sh +
+                 static_cast<int64_t>(q0 + kk) * p.dq_ss;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int d = rb + 8 * j;
+      if (d < D) dqr[d] = dq[j] * p.scale;
+    }
+  }
+}
+
+template <int DP, bool SOFTCAP>
+void launch_f32_dp(const BwdParams& p, hipStream_t s) {
+  const int grid_dkv = p.B * p.Hkv * ((p.Skv + kF32T - 1) / kF32T);
+  const int grid_dq = p.B * p.Hq * ((p.Sq + kF32T - 1) / kF32T);
+  if (grid_dkv > 0) {
+    hipLaunchKernelGGL((bwd_f32_dkdv_kernel<DP, SOFTCAP>), dim3(grid_dkv), dim3(kThreads), 0, s, p);
+  }
+  hipLaunchKernelGGL((bwd_f32_dq_kernel<DP, SOFTCAP>), dim3(grid_dq), dim3(kThreads), 0, s, p);
+}
+
+void launch_f32(const BwdParams& p, bool softcap, int grid_pre, hipStream_t s) {
+  hipLaunchKernelGGL((bwd_pre_kernel<F32Tag>), dim3(grid_pre), dim3(kThreads), 0, s, p);
+  if (p.D <= 64) {
+    softcap ? launch_f32_dp<64, true>(p, s) : launch_f32_dp<64, false>(p, s);
+  } else if (p.D <= 128) {
+    softcap ? launch_f32_dp<128, true>(p, s) : launch_f32_dp<128, false>(p, s);
+  } else {
+    softcap ? launch_f32_dp<256, true>(p, s) : launch_f32_dp<256, false>(p, s);
   }
 }
 
@@ -696,9 +981,15 @@ void launch_tag(const BwdParams& p, bool softcap, int grid_pre, int grid_dkv, in
   if (p.D <= 64) {
     softcap ? launch_main<Tag, 64, true>(p, grid_dkv, grid_dq, s)
             : launch_main<Tag, 64, false>(p, grid_dkv, grid_dq, s);
-  } else {
+  } else if (p.D <= 128) {
     softcap ? launch_main<Tag, 128, true>(p, grid_dkv, grid_dq, s)
             : launch_main<Tag, 128, false>(p, grid_dkv, grid_dq, s);
+  } else if (p.D <= 192) {
+    softcap ? launch_main<Tag, 192, true>(p, grid_dkv, grid_dq, s)
+            : launch_main<Tag, 192, false>(p, grid_dkv, grid_dq, s);
+  } else {
+    softcap ? launch_main<Tag, 256, true>(p, grid_dkv, grid_dq, s)
+            : launch_main<Tag, 256, false>(p, grid_dkv, grid_dq, s);
   }
 }
 
@@ -792,7 +1083,13 @@ int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream) {
   p.xcd_remap_dkv = bwd_xcd_remap(grid_dkv);
   p.xcd_group_dq = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_q, p.n_qt);
   p.xcd_group_dkv = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_kv, p.n_kt);
-  if (a.dtype == FFA_DTYPE_BF16) {
+  if (a.dtype == FFA_DTYPE_FP32) {
+    // 32-row / 32-key workgroups
+    const int64_t g32 = static_cast<int64_t>(a.batch) * a.heads_q * ((a.seqlen_q + 31) / 32) +
+                        static_cast<int64_t>(a.batch) * a.heads_kv * ((a.seqlen_kv + 31) / 32);
+    if (g32 > 0x7fffffff) return FFA_ERR_TOO_LARGE;
+    launch_f32(p, softcap, static_cast<int>(grid_pre), stream);
+  } else if (a.dtype == FFA_DTYPE_BF16) {
     launch_tag<Bf16Tag>(p, softcap, static_cast<int>(grid_pre), static_cast<int>(grid_dkv),
                         static_cast<int>(grid_dq), stream);
   } else {

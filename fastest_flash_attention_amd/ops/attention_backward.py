@@ -83,9 +83,9 @@ def fastest_flash_attn_backward(
     dtype = q.dtype
     if not (k.dtype == v.dtype == output.dtype == grad_output.dtype == dtype):
         raise TypeError("grad_output, q, k, v and output must share one dtype")
-    code = _lib.dtype_code(dtype)  # bf16 / fp16 (TypeError otherwise)
-    if D > 128:
-        raise ValueError(f"head_dim {D} > 128 is not supported by the backward kernel")
+    code = _lib.dtype_code(dtype, allow_fp32=True)  # bf16 / fp16 / fp32 (TypeError otherwise)
+    if D > 256:
+        raise ValueError(f"head_dim {D} > 256 is not supported by the backward kernels")
     if sliding_window is not None and int(sliding_window) <= 0:
         raise ValueError("sliding_window must be positive")
     if softcap is not None and float(softcap) <= 0.0:

@@ -70,7 +70,7 @@ typedef enum ffa_status {
 typedef enum ffa_dtype {
   FFA_DTYPE_BF16 = 0,
   FFA_DTYPE_FP16 = 1,
-  FFA_DTYPE_FP32 = 2   /* ffa_prefill_fwd only: fp32 MFMA, fp32 output */
+  FFA_DTYPE_FP32 = 2   /* ffa_prefill_fwd (fp32 MFMA) and ffa_attn_bwd (fp32 FMA) only */
 } ffa_dtype;
 
 /*
@@ -336,8 +336,9 @@ int ffa_mla_decode_fwd(const ffa_mla_decode_args* args, void* stream);
  * GQA: dK / dV of kv head j sum over the q heads j * ratio .. (j + 1) * ratio - 1.
  * Layout: element strides [batch, head, seq, dim] (dim stride 1; dq/dk/dv written in
  * place, no broadcast strides on them); lse strides [batch, head, seq]. All of dout,
- * q, k, v, o, dq, dk, dv share the dtype (bf16 / fp16: fp32 accumulation, P and dS
- * rounded to the dtype for the matrix products). head_dim is 1..128 and a multiple of
+ * q, k, v, o, dq, dk, dv share the dtype: bf16 / fp16 (MFMA with fp32 accumulation, P
+ * and dS rounded to the dtype for the matrix products) or fp32 (fp32 FMAs throughout,
+ * as the reference computes fp32 inputs). head_dim is 1..256 and a multiple of
  * 8; every tensor is 16-byte aligned with batch/head/seq strides multiples of 8
  * elements (FFA_ERR_MISALIGNED) and seq strides below 2^24 elements. The workspace
  * (16-byte aligned, ffa_attn_bwd_workspace_bytes()) holds per-row statistics; the
@@ -370,13 +371,13 @@ typedef struct ffa_attn_bwd_args {
   int32_t heads_kv;
   int32_t seqlen_q;
   int32_t seqlen_kv;
-  int32_t head_dim;         /* 1..128 */
+  int32_t head_dim;         /* 1..256 */
   int32_t q_offset;
   int32_t causal;
   int32_t window;           /* <= 0: no sliding window */
   float scale;              /* any finite value */
-  float softcap;            /* <= 0: no softcap */
-  int32_t dtype;            /* FFA_DTYPE_BF16 or FFA_DTYPE_FP16 */
+  float softcap;            /* <= 0: no softcap; else finite */
+  int32_t dtype;            /* ffa_dtype */
 } ffa_attn_bwd_args;
 
 size_t ffa_attn_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q);

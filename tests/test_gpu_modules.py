@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import copy
+
 import pytest
 import torch
 
@@ -110,3 +112,46 @@ def test_training_mode_forward_and_backward():
         err = (got - want).abs()
         assert err.max() <= 5e-2 * want.abs().max(), (err.max(), want.abs().max())
         assert err.mean() <= 2e-2 * want.abs().mean(), (err.mean(), want.abs().mean())
+
+
+def test_mla_training_mode_backward_d192():
+    """The MLA module trains through the HIP backward at D = head_dim + rope_dim = 192:
+    the loss gradient reaches the input and every projection weight and matches a fp32
+    CPU restatement (the module's own projections and RoPE on an fp32 copy of its
+    weights, textbook causal softmax attention over the zero-padded V)."""
+    require_gpu()
+    torch.manual_seed(4)
+    m = ffa.FastestFlashMLA(hidden_size=256, num_heads=2, head_dim=128, latent_dim=64,
+                            rope_dim=64).cuda().to(torch.bfloat16)
+    m.train()
+    B, S = 2, 70
+    x = torch.randn(B, S, 256, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    g = torch.randn(B, S, 256, dtype=torch.bfloat16)
+    say("module MLA training-mode forward + backward (D = 192)")
+    out = m(x)
+    assert out.shape == (B, S, 256)
+    out.backward(g.cuda())
+    torch.cuda.synchronize()
+
+    mr = copy.deepcopy(m).float().cpu()
+    mr.zero_grad(set_to_none=True)
+    xr = x.detach().float().cpu().requires_grad_()
+    q, k, vp = mr.project_qkv(xr)
+    assert q.shape[-1] == 192
+    s = (q @ k.transpose(-1, -2)) * mr.scale
+    mask = torch.triu(torch.ones(S, S, dtype=torch.bool), diagonal=1)
+    p = torch.softmax(s.masked_fill(mask, float("-inf")), dim=-1)
+    a = (p @ vp).transpose(1, 2).reshape(B, S, -1)
+    ref = mr.o_proj(a)
+    ref.backward(g.float())
+    grads = dict(mr.named_parameters())
+    pairs = [("out", out, ref), ("x", x.grad, xr.grad)]
+    pairs += [(n, p_.grad, grads[n].grad) for n, p_ in m.named_parameters()]
+    for name, got, want in pairs:
+        assert got is not None and want is not None, name
+        got = got.detach().float().cpu()
+        want = want.detach()
+        err = (got - want).abs()
+        print(f"  {name}: max err {err.max():.3e} (ref max {want.abs().max():.3e})", flush=True)
+        assert err.max() <= 5e-2 * want.abs().max(), (name, err.max(), want.abs().max())
+        assert err.mean() <= 2e-2 * want.abs().mean(), (name, err.mean(), want.abs().mean())

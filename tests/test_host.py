@@ -217,10 +217,10 @@ def test_validation_errors_without_device(lib):
     assert lib.ffa_mla_decode_fwd(ctypes.byref(m), None) == -1
     bw = _lib.AttnBwdArgs()
     assert lib.ffa_attn_bwd(None, None) == -1
-    bw.dtype, bw.head_dim, bw.batch, bw.heads_q, bw.heads_kv = 2, 64, 1, 4, 2
-    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -2  # no fp32 backward kernel
-    bw.dtype, bw.head_dim = 0, 192
-    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -3  # head_dim <= 128
+    bw.dtype, bw.head_dim, bw.batch, bw.heads_q, bw.heads_kv = 3, 64, 1, 4, 2
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -2  # bf16 / fp16 / fp32 only
+    bw.dtype, bw.head_dim = 0, 264
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -3  # head_dim <= 256
     bw.head_dim, bw.heads_q = 64, 3
     assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -5
     bw.heads_q, bw.seqlen_q, bw.seqlen_kv = 4, 100, 100
