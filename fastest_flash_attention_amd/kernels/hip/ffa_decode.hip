@@ -474,6 +474,76 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams 
   }
 }
 
+// Split-K merge of the MLA decode for up to NS splits: one wave per (sequence, query
+// head), lane l owns latent dims 8l .. 8l + 7 (one 16-byte read per split). Every read
+// it needs (the context length, each split's lse and 16-bit partial row) is issued at
+// once, so the merge costs one memory round trip rather than three dependent ones
+// (length, then lse, then partials); splits past the sequence's length are read (the
+// workspace holds n_splits rows per head) and given weight 0.
+template <typename Tag, int NS>
+__global__ __launch_bounds__(256) void mla_combine_kernel(const DecodeParams p) {
+  using E = Elem<Tag>;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.x * 4 + wave;
+  if (bh >= p.B * p.Hq) return;  // wave-uniform; the kernel has no barrier
+  const int b = bh / p.Hq;
+  const int hq = bh - b * p.Hq;
+  const int64_t base = static_cast<int64_t>(bh) * p.n_splits;
+  const float* lse_row = p.ws_lse + base;
+  const int d0 = 8 * lane;
+  const bool dlive = d0 < p.D;  // D is a multiple of 8
+  const int len = p.lens[b];
+  float ls[NS];
+  u32x4 v[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool in = s < p.n_splits;
+    ls[s] = in ? lse_row[s] : kNegInf;
+    v[s] = (in && dlive) ? *reinterpret_cast<const u32x4*>(p.ws_o16 + (base + s) * p.dp + d0)
+                         : u32x4{0u, 0u, 0u, 0u};
+  }
+  const int L = min(max(len, 0), p.max_len);
+  const int s1 = L > 0 ? (L + p.tps - 1) / p.tps : 0;  // splits that ran (no window)
+  float mm = kNegInf;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) mm = s < s1 ? fmaxf(mm, ls[s]) : mm;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.0f;
+  if (mm != kNegInf) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bool use = s < s1;
+      const float w = use ? __expf(ls[s] - mm) : 0.0f;  // exp(-inf) = 0 for empty partials
+      wsum += w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t word = v[s][e >> 1];
+        const float x = E::to_f32(static_cast<uint16_t>((e & 1) ? (word >> 16) : (word & 0xffffu)));
+        acc[e] = fmaf(w, use ? x : 0.0f, acc[e]);
+      }
+    }
+  }
+  const bool ok = mm != kNegInf && wsum > 0.0f;
+  const float inv = ok ? 1.0f / wsum : 0.0f;
+  uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh;
+  if (dlive) {
+    const u32x4 out = {E::pack2(acc[0] * inv, acc[1] * inv), E::pack2(acc[2] * inv, acc[3] * inv),
+                       E::pack2(acc[4] * inv, acc[5] * inv), E::pack2(acc[6] * inv, acc[7] * inv)};
+    if ((reinterpret_cast<uintptr_t>(orow) & 15u) == 0) {
+      *reinterpret_cast<u32x4*>(orow + d0) = out;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        orow[d0 + e] = static_cast<uint16_t>((e & 1) ? (out[e >> 1] >> 16) : (out[e >> 1] & 0xffffu));
+      }
+    }
+  }
+  if (lane == 0 && p.lse != nullptr) {
+    p.lse[b * p.l_sb + hq * p.l_sh] = ok ? mm + logf(wsum) : kNegInf;
+  }
+}
+
 // ---------------------------------------------------------------------------------
 // MLA decode over the compressed latent cache (absorbed form of the reference
 // FastestFlashMLA attention, modules/flash_mla.py:116-172). With W_uk / W_uv the
@@ -1150,8 +1220,16 @@ void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3
       hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256, false>), grid, dim3(kMlaThreads), 0, s, mp);
     }
   }
-  // one wave per 128-dim slice of the dim_v = 256 or 512 latent output dims
-  hipLaunchKernelGGL((decode_combine_kernel<Tag, true>), dim3(cp.B * cp.Hq), dim3(dim_v / 2), 0, s, cp);
+  const unsigned heads4 = static_cast<unsigned>((static_cast<int64_t>(cp.B) * cp.Hq + 3) / 4);
+  if (cp.n_splits <= 8) {
+    hipLaunchKernelGGL((mla_combine_kernel<Tag, 8>), dim3(heads4), dim3(256), 0, s, cp);
+  } else if (cp.n_splits <= 16) {
+    hipLaunchKernelGGL((mla_combine_kernel<Tag, 16>), dim3(heads4), dim3(256), 0, s, cp);
+  } else {
+    // many splits: one wave per 128-dim slice of the latent output dims, splits walked in
+    // groups of eight
+    hipLaunchKernelGGL((decode_combine_kernel<Tag, true>), dim3(cp.B * cp.Hq), dim3(dim_v / 2), 0, s, cp);
+  }
 }
 
 }  // namespace
