@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+from dataclasses import dataclass
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -48,7 +49,20 @@ def mla_decode_workspace_bytes(batch: int, heads_q: int, dim_v: int, max_context
         batch, heads_q, dim_v, max_context_len, tokens_per_split))
 
 
-def fastest_flash_mla_decode(
+@dataclass
+class MlaDecodeCall:
+    """A fully resolved MLA decode launch: the ABI struct plus the tensors it points to
+    (kept alive with it). ``launch_mla_decode`` runs it on the current stream; a serving
+    loop that refills q / context_lens in place can launch the same call every step."""
+
+    args: _lib.MlaDecodeArgs
+    q: torch.Tensor
+    out: torch.Tensor
+    lse: Optional[torch.Tensor]
+    keep: tuple = ()
+
+
+def prepare_mla_decode(
     q: torch.Tensor,
     kv_pages: torch.Tensor,
     block_tables: torch.Tensor,
@@ -61,17 +75,10 @@ def fastest_flash_mla_decode(
     tokens_per_split: Optional[int] = None,
     workspace: Optional[torch.Tensor] = None,
     check_block_tables: bool = False,
-) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """Latent-space attention of one query token per sequence.
-
-    Page ids outside the pool exclude the tokens they would hold, or raise IndexError
-    with ``check_block_tables=True`` (as for ``fastest_flash_paged_decode``).
-
-    q: ``[B, H, dim_v + 64]`` absorbed queries ``[W_uk^T q_nope, q_rope]``; kv_pages:
-    ``[num_pages, page_size, dim_v + 64]`` rows ``[c_t | r_t]``; block_tables int32
-    ``[B, max_blocks]``; context_lens int32 ``[B]``. Sequence b attends to its first
-    ``context_lens[b]`` tokens. Returns ``(o_lat [B, H, dim_v], lse [B, H] or None)``.
-    """
+    out: Optional[torch.Tensor] = None,
+) -> MlaDecodeCall:
+    """Check the arguments of ``fastest_flash_mla_decode``, allocate outputs (or take
+    ``out``) and the workspace, build the ABI struct. Launches nothing."""
     if q.dim() != 3 or kv_pages.dim() != 3:
         raise ValueError("q must be [B, H, dim_v + 64] and kv_pages [num_pages, page_size, dim_v + 64]")
     B, H, dqk = q.shape
@@ -105,7 +112,12 @@ def fastest_flash_mla_decode(
         tokens_per_split = _auto_mla_tokens_per_split(B, (H + 31) // 32, max_context_len)
 
     lib = _lib.load()
-    out = torch.empty((B, H, dim_v), dtype=q.dtype, device=q.device)
+    if out is None:
+        out = torch.empty((B, H, dim_v), dtype=q.dtype, device=q.device)
+    elif (tuple(out.shape) != (B, H, dim_v) or out.dtype != q.dtype or out.device != q.device
+          or out.stride(-1) != 1 or out.data_ptr() % 4):
+        raise ValueError(f"out must be a [B, H, dim_v] {q.dtype} tensor on {q.device} with "
+                         f"unit last stride")
     lse = torch.empty((B, H), dtype=torch.float32, device=q.device) if return_lse else None
     need = int(lib.ffa_mla_decode_workspace_bytes(B, H, dim_v, max_context_len, tokens_per_split))
     if workspace is None or workspace.numel() * workspace.element_size() < need:
@@ -135,11 +147,49 @@ def fastest_flash_mla_decode(
     a.tokens_per_split = int(tokens_per_split)
     a.scale = float(scale)
     a.dtype = code
-    stream = _lib.current_stream_handle(q.device)
-    with torch.cuda.device(q.device):
-        rc = lib.ffa_mla_decode_fwd(ctypes.byref(a), ctypes.c_void_p(stream))
+    return MlaDecodeCall(args=a, q=q, out=out, lse=lse,
+                         keep=(kv_pages, block_tables, context_lens, workspace))
+
+
+def launch_mla_decode(call: MlaDecodeCall) -> None:
+    lib = _lib.load()
+    stream = _lib.current_stream_handle(call.q.device)
+    with torch.cuda.device(call.q.device):
+        rc = lib.ffa_mla_decode_fwd(ctypes.byref(call.args), ctypes.c_void_p(stream))
     _lib.check(rc)
-    return out, lse
+
+
+def fastest_flash_mla_decode(
+    q: torch.Tensor,
+    kv_pages: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    *,
+    dim_v: int,
+    scale: float,
+    return_lse: bool = False,
+    max_context_len: Optional[int] = None,
+    tokens_per_split: Optional[int] = None,
+    workspace: Optional[torch.Tensor] = None,
+    check_block_tables: bool = False,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Latent-space attention of one query token per sequence.
+
+    Page ids outside the pool exclude the tokens they would hold, or raise IndexError
+    with ``check_block_tables=True`` (as for ``fastest_flash_paged_decode``).
+
+    q: ``[B, H, dim_v + 64]`` absorbed queries ``[W_uk^T q_nope, q_rope]``; kv_pages:
+    ``[num_pages, page_size, dim_v + 64]`` rows ``[c_t | r_t]``; block_tables int32
+    ``[B, max_blocks]``; context_lens int32 ``[B]``. Sequence b attends to its first
+    ``context_lens[b]`` tokens. Returns ``(o_lat [B, H, dim_v], lse [B, H] or None)``.
+    """
+    call = prepare_mla_decode(q, kv_pages, block_tables, context_lens, dim_v=dim_v,
+                              scale=scale, return_lse=return_lse,
+                              max_context_len=max_context_len,
+                              tokens_per_split=tokens_per_split, workspace=workspace,
+                              check_block_tables=check_block_tables)
+    launch_mla_decode(call)
+    return call.out, call.lse
 
 
 class MLALatentCache:

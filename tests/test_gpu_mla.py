@@ -157,3 +157,23 @@ def test_mla_decode_rejects_bad_shapes():
     with pytest.raises(RuntimeError):  # a CPU query: there is no CPU path
         ffa.fastest_flash_mla_decode(torch.zeros(1, 4, 576, dtype=BF16),
                                      pool.new_zeros(2, 16, 576), bt, lens, dim_v=512, scale=0.1)
+
+
+def test_prepared_mla_call_matches_one_shot():
+    """prepare_mla_decode once + launch_mla_decode per step (the serving loop form) gives
+    the one-shot call's result, also after q is refilled in place."""
+    require_gpu()
+    from fastest_flash_attention_amd.ops.mla_decode import launch_mla_decode, prepare_mla_decode
+    lens = [300, 45, 1]
+    q, pool, bt, lens_t = _paged_case(21, lens, 16, 512, 32, BF16)
+    q, pool, bt, lens_t = q.cuda(), pool.cuda(), bt.cuda(), lens_t.cuda()
+    say("mla decode prepared call")
+    call = prepare_mla_decode(q, pool, bt, lens_t, dim_v=512, scale=0.06, return_lse=True)
+    for seed in (0, 1):
+        if seed:
+            q.copy_(torch.randn(q.shape, generator=torch.Generator().manual_seed(seed)).to(BF16))
+        launch_mla_decode(call)
+        o, lse = ffa.fastest_flash_mla_decode(q, pool, bt, lens_t, dim_v=512, scale=0.06,
+                                              return_lse=True)
+        torch.cuda.synchronize()
+        assert torch.equal(call.out, o) and torch.equal(call.lse, lse)
