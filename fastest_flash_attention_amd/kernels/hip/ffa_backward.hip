@@ -33,7 +33,8 @@
 // free of LDS bank conflicts.
 // P and dS are rounded to the input's 16-bit type for the MFMAs; everything else is
 // fp32. Inputs are 16-byte aligned with head_dim % 8 == 0 (the host pads otherwise);
-// head_dim up to 128.
+// head_dim up to 256 (kernel widths 64, 128, 192, 256). fp32 inputs run the FMA
+// kernels at the end of this file, with the same decomposition and no rounding.
 
 #include <type_traits>
 
