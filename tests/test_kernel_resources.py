@@ -1,0 +1,77 @@
+"""Register-spill guard (CPU, no GPU needed): compile the prefill, decode and backward
+translation units for gfx950 with the library's own flags and read every kernel's
+private-segment (scratch) size from the code-object metadata.
+
+Scratch reloads inside a kernel's KV loop come with `s_waitcnt vmcnt` waits that also
+wait on the in-flight direct-to-LDS tile loads (the kernels issue those from inline asm,
+invisible to the compiler's wait counting), which cost the prefill 15 % when it spilled.
+So every hot kernel must stay spill-free; the known exceptions are listed with a bound.
+"""
+
+from __future__ import annotations
+
+import os
+import re
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+
+from fastest_flash_attention_amd.kernels.hip import build
+
+# kernel-name regex -> largest scratch bytes per lane allowed
+EXCEPTIONS = {
+    # head_dim 192 with softcap: the tanh work of 32-key tiles at 256 VGPRs
+    r"prefill_kernel<.*, 192, 32, true>": 16,
+    # head_dim 256 dK/dV: 2 x 32 keys x 256 dims of fp32 accumulators per wave
+    r"bwd_dkdv_kernel<.*, 256, (true|false)>": 512,
+}
+
+
+def _scratch_by_kernel(src: str, tmp: str) -> dict:
+    out = os.path.join(tmp, os.path.basename(src) + ".s")
+    cmd = [build.hipcc(), *build.HIPCC_FLAGS, f"-I{build.INCLUDE}", f"-I{build.HERE}",
+           "--cuda-device-only", "-S", src, "-o", out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    text = open(out).read()
+    res = {}
+    for block in text.split("\n  - .agpr_count:")[1:]:
+        name = re.search(r"\.name:\s+(\S+)", block).group(1)
+        priv = int(re.search(r"\.private_segment_fixed_size:\s+(\d+)", block).group(1))
+        res[name] = priv
+    return res
+
+
+def _demangle(names):
+    cxxfilt = shutil.which("c++filt") or shutil.which("llvm-cxxfilt")
+    if cxxfilt is None:
+        return {n: n for n in names}
+    r = subprocess.run([cxxfilt], input="\n".join(names), capture_output=True, text=True)
+    return dict(zip(names, r.stdout.splitlines()))
+
+
+@pytest.mark.skipif(shutil.which("hipcc") is None and not os.path.exists("/opt/rocm/bin/hipcc"),
+                    reason="hipcc not installed")
+def test_hot_kernels_do_not_spill(tmp_path):
+    srcs = [os.path.join(build.HERE, f) for f in
+            ("ffa_prefill.hip", "ffa_decode.hip", "ffa_backward.hip")]
+    with ThreadPoolExecutor(3) as ex:
+        parts = list(ex.map(lambda s: _scratch_by_kernel(s, str(tmp_path)), srcs))
+    scratch = {k: v for part in parts for k, v in part.items()}
+    assert len(scratch) >= 60, f"only {len(scratch)} kernels found"
+    names = _demangle(list(scratch))
+    bad = []
+    for mangled, priv in scratch.items():
+        name = names[mangled]
+        limit = 0
+        for pat, lim in EXCEPTIONS.items():
+            if re.search(pat, name):
+                limit = lim
+        if priv > limit:
+            bad.append(f"{name}: {priv} B scratch per lane (allowed {limit})")
+    assert not bad, "\n".join(bad)
+    # the headline kernel in particular
+    ns = [n for m, n in names.items() if re.search(r"prefill_kernel<ffa::Bf16Tag, 128, 64, false>", n)]
+    assert ns and all(scratch[m] == 0 for m, n in names.items() if n in ns)
