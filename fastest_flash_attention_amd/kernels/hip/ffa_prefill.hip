@@ -372,21 +372,38 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
                                        (p.window > 0 && kt0 < qwl_abs - p.window + 1) ||
                                        kpartial);
     if (need_mask) {
-      // keys kt0 .. kt0 + BN - 1 of the block mask (BN divides 64, kt0 % BN == 0)
-      // pre-shifted by this lane half's key offset 4g, so each element tests a bit at
-      // a compile-time position (no per-element 64-bit shift constants to hold)
-      const uint64_t kbits =
-          p.kmask != nullptr ? kmask_row[kt0 >> 6] >> ((kt0 & 63) + 4 * g) : ~uint64_t{0};
       const int key0 = kt0 + 4 * g;
+      // (not in the three-workgroup head_dim 64 kernel: its 168-VGPR budget spills with
+      // both paths)
+      if (kMinBlocks<DP, SOFTCAP> <= 2 && p.kmask == nullptr && p.window <= 0 && kt0 + BN <= Skv) {
+        // Causal edge only (the common masked tile: the diagonal of a causal sweep):
+        // element (key0 + off) is visible iff off <= qa - key0, one compare against a
+        // compile-time offset per score instead of the general test below.
+        const int lim = qa - key0;
 #pragma unroll
-      for (int nb = 0; nb < S::NB; ++nb) {
+        for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
-          const int key = key0 + off;
-          const bool ok = key < Skv && (!p.causal || key <= qa) &&
-                          (p.window <= 0 || key >= qa - p.window + 1) && ((kbits >> off) & 1u);
-          sacc[nb][r] = ok ? sacc[nb][r] : kNegInf;
+          for (int r = 0; r < 16; ++r) {
+            const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
+            sacc[nb][r] = off <= lim ? sacc[nb][r] : kNegInf;
+          }
+        }
+      } else {
+        // keys kt0 .. kt0 + BN - 1 of the block mask (BN divides 64, kt0 % BN == 0)
+        // pre-shifted by this lane half's key offset 4g, so each element tests a bit at
+        // a compile-time position (no per-element 64-bit shift constants to hold)
+        const uint64_t kbits =
+            p.kmask != nullptr ? kmask_row[kt0 >> 6] >> ((kt0 & 63) + 4 * g) : ~uint64_t{0};
+#pragma unroll
+        for (int nb = 0; nb < S::NB; ++nb) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
+            const int key = key0 + off;
+            const bool ok = key < Skv && (!p.causal || key <= qa) &&
+                            (p.window <= 0 || key >= qa - p.window + 1) && ((kbits >> off) & 1u);
+            sacc[nb][r] = ok ? sacc[nb][r] : kNegInf;
+          }
         }
       }
     }
