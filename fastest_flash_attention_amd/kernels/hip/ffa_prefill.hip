@@ -375,17 +375,30 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       const int key0 = kt0 + 4 * g;
       // (not in the three-workgroup head_dim 64 kernel: its 168-VGPR budget spills with
       // both paths)
-      if (kMinBlocks<DP, SOFTCAP> <= 2 && p.kmask == nullptr && p.window <= 0 && kt0 + BN <= Skv) {
-        // Causal edge only (the common masked tile: the diagonal of a causal sweep):
-        // element (key0 + off) is visible iff off <= qa - key0, one compare against a
-        // compile-time offset per score instead of the general test below.
-        const int lim = qa - key0;
+      if (kMinBlocks<DP, SOFTCAP> <= 2 && p.kmask == nullptr && kt0 + BN <= Skv) {
+        // Causal / window edges of a full tile without a block mask (the diagonal of a
+        // causal sweep, the left edge of a window): element (key0 + off) is visible iff
+        // lo <= off <= hi, compares against a compile-time offset per score instead of
+        // the general test below.
+        const int hi = p.causal ? qa - key0 : 0x7fffffff;
+        if (p.window <= 0) {
 #pragma unroll
-        for (int nb = 0; nb < S::NB; ++nb) {
+          for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
-            sacc[nb][r] = off <= lim ? sacc[nb][r] : kNegInf;
+            for (int r = 0; r < 16; ++r) {
+              const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
+              sacc[nb][r] = off <= hi ? sacc[nb][r] : kNegInf;
+            }
+          }
+        } else {
+          const int lo = qa - p.window + 1 - key0;
+#pragma unroll
+          for (int nb = 0; nb < S::NB; ++nb) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
+              sacc[nb][r] = (off >= lo && off <= hi) ? sacc[nb][r] : kNegInf;
+            }
           }
         }
       } else {
