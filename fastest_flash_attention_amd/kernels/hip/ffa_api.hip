@@ -9,6 +9,7 @@
 #include <cmath>
 
 #include "ffa.h"
+#include "ffa_common.h"
 #include "ffa_internal.h"
 
 namespace {
@@ -146,7 +147,7 @@ int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
   }
   // Positions are int32 inside the kernel.
   const int64_t max_pos = static_cast<int64_t>(a->q_offset) + a->seqlen_q;
-  if (max_pos > 0x3fffffff || a->seqlen_kv > 0x3fffffff || a->q_offset < -0x3fffffff) {
+  if (max_pos > ffa::kMaxPos || a->seqlen_kv > ffa::kMaxPos || a->q_offset < -ffa::kMaxPos) {
     return FFA_ERR_TOO_LARGE;
   }
   return ffa::launch_prefill(*a, static_cast<hipStream_t>(stream));
@@ -310,7 +311,7 @@ int ffa_attn_bwd(const ffa_attn_bwd_args* a, void* stream) {
     return FFA_ERR_TOO_LARGE;
   }
   const int64_t max_pos = static_cast<int64_t>(a->q_offset) + a->seqlen_q;
-  if (max_pos > 0x3fffffff || a->seqlen_kv > 0x3fffffff || a->q_offset < -0x3fffffff) {
+  if (max_pos > ffa::kMaxPos || a->seqlen_kv > ffa::kMaxPos || a->q_offset < -ffa::kMaxPos) {
     return FFA_ERR_TOO_LARGE;
   }
   const size_t need = ffa::attn_bwd_workspace_bytes(a->batch, a->heads_q, a->seqlen_q);

@@ -500,11 +500,15 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
       }
     }
     if (need_mask) {
+      // row qa0 + off (off = 8 (r >> 2) + (r & 3), a compile-time offset) sees this
+      // lane's key iff lo <= off <= hi: causal key <= row, window key >= row - w + 1
       const int qa0 = q0_abs + 4 * g;
+      const int lo = p.causal ? key - qa0 : -0x7fffffff;
+      const int hi = p.window > 0 ? key + p.window - 1 - qa0 : 0x7fffffff;  // window clamped on the host
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int qa = qa0 + 8 * (r >> 2) + (r & 3);
-        const bool ok = (!p.causal || key <= qa) && (p.window <= 0 || key >= qa - p.window + 1);
+        const int off = 8 * (r >> 2) + (r & 3);
+        const bool ok = (off >= lo) & (off <= hi);
         pv[r] = ok ? pv[r] : 0.0f;
         dsv[r] = ok ? dsv[r] : 0.0f;
       }
@@ -694,14 +698,17 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
       }
     }
     if (need_mask) {
+      // key key0 + off (off a compile-time offset) is visible to this lane's row iff
+      // off <= hi (below Skv and, causal, at or before the row) and off >= lo (window)
       const int key0 = kt0 + 4 * g;
+      const int hi = min(Skv - 1, p.causal ? qa : 0x7fffffff) - key0;
+      const int lo = p.window > 0 ? qa - p.window + 1 - key0 : -0x7fffffff;  // window clamped on the host
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int kk = key0 + 32 * nb + 8 * (r >> 2) + (r & 3);
-          const bool ok = kk < Skv && (!p.causal || kk <= qa) &&
-                          (p.window <= 0 || kk >= qa - p.window + 1);
+          const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
+          const bool ok = (off >= lo) & (off <= hi);
           dsv[nb][r] = ok ? dsv[nb][r] : 0.0f;
         }
       }
@@ -1050,9 +1057,7 @@ int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream) {
   p.D = a.head_dim;
   p.q_offset = a.q_offset;
   p.causal = a.causal ? 1 : 0;
-  // a window of 2^30 or more masks nothing (positions are below 2^30); clamping it
-  // keeps every position - window + 1 inside int32
-  p.window = a.window > 0 ? min(a.window, 0x40000000) : 0;
+  p.window = clamp_window(a.window, a.q_offset, a.seqlen_q);
   p.ratio = a.heads_q / a.heads_kv;
   p.sq_pad = static_cast<int>(sq_padded(a.seqlen_q));
   p.n_qt = p.sq_pad / kQTile;

@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
             }
           }
         } else {
-          const int lo = qa - p.window + 1 - key0;
+          const int lo = qa - p.window + 1 - key0;  // no overflow: the host clamps the window
 #pragma unroll
           for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
@@ -897,7 +897,7 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   p.D = a.head_dim;
   p.q_offset = a.q_offset;
   p.causal = a.causal ? 1 : 0;
-  p.window = a.window > 0 ? a.window : 0;
+  p.window = clamp_window(a.window, a.q_offset, a.seqlen_q);
   p.ratio = a.heads_q / a.heads_kv;
   p.n_qt = (a.seqlen_q + kBlockM - 1) / kBlockM;
   const bool softcap = a.softcap > 0.0f;

@@ -102,7 +102,9 @@ typedef enum ffa_dtype {
  * [batch, head, seq]. q/k/v/o share the dtype (bf16 / fp16 on bf16 / fp16 MFMA with
  * fp32 softmax and accumulation; fp32 on fp32 MFMA). q/k/v/o are 16-byte aligned, head_dim
  * and the batch/head/seq strides are multiples of 8 elements (FFA_ERR_MISALIGNED
- * otherwise), and k/v seq strides are below 2^24 elements.
+ * otherwise), and k/v seq strides are below 2^24 elements. Positions are 32-bit in the
+ * kernels: |q_offset|, q_offset + seqlen_q and seqlen_kv must not exceed 2^29 - 1
+ * (FFA_ERR_TOO_LARGE; the same for ffa_attn_bwd).
  */
 typedef struct ffa_prefill_args {
   const void* q;

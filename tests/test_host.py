@@ -418,3 +418,16 @@ def test_check_page_ids():
                        torch.tensor([0, 12], dtype=torch.int32), 4, 8, 12)
     with pytest.raises(IndexError):
         check_page_ids(bt, torch.tensor([9, 0], dtype=torch.int32), 4, 7, 9)  # 7 >= 7 pages
+
+
+@pytest.mark.parametrize("field,value", [
+    ("q_offset", -(1 << 29)),          # |q_offset| > 2^29 - 1
+    ("q_offset", (1 << 29) - 64),      # q_offset + seqlen_q > 2^29 - 1
+    ("seqlen_kv", 1 << 29),
+])
+def test_abi_rejects_positions_beyond_int32_range(lib, field, value):
+    """Positions and window bounds are int32 in the kernels: the prefill rejects position
+    ranges beyond 2^29 - 1 before any HIP call (FFA_ERR_TOO_LARGE)."""
+    a = _valid_prefill_args(0.125)
+    setattr(a, field, value)
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -9
