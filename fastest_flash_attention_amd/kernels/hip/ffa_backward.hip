@@ -33,8 +33,9 @@
 // free of LDS bank conflicts.
 // P and dS are rounded to the input's 16-bit type for the MFMAs; everything else is
 // fp32. Inputs are 16-byte aligned with head_dim % 8 == 0 (the host pads otherwise);
-// head_dim up to 256 (kernel widths 64, 128, 192, 256). fp32 inputs run the FMA
-// kernels at the end of this file, with the same decomposition and no rounding.
+// head_dim up to 256 (kernel widths 64, 128, 192, 256). fp32 inputs run the fp32
+// kernels at the end of this file (fp32 MFMA up to head_dim 128, FMA above), with no
+// rounding.
 
 #include <type_traits>
 
@@ -737,8 +738,9 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
 }
 
 // ---------------------------------------------------------------------------------
-// fp32 inputs: the reference computes them in fp32 (cpu_reference.py:319-427), so they
-// run on fp32 FMAs. A workgroup (256 threads) owns 32 keys (dK / dV) or 32 query rows
+// fp32 inputs with head_dim > 128: the reference computes them in fp32
+// (cpu_reference.py:319-427), so they run on fp32 FMAs (head_dim <= 128 runs the MFMA
+// kernels below). A workgroup (256 threads) owns 32 keys (dK / dV) or 32 query rows
 // (dQ) and sweeps 32-row tiles of the other side through LDS, rows padded by one float
 // so the 32 rows read together at one dim fall in 32 distinct banks. Per tile, thread t
 // computes the scores of key (or row) t % 32 against rows t / 32 + 8 i (i < 4), and
@@ -963,12 +965,413 @@ void launch_f32_dp(const BwdParams& p, hipStream_t s) {
   hipLaunchKernelGGL((bwd_f32_dq_kernel<DP, SOFTCAP>), dim3(grid_dq), dim3(kThreads), 0, s, p);
 }
 
+// ---------------------------------------------------------------------------------
+// fp32 inputs up to head_dim 128 on v_mfma_f32_32x32x2_f32 (fp32 operands, no
+// rounding). A workgroup of 4 waves owns 32 keys (dK / dV) or 32 query rows (dQ); its
+// waves split the other side's 32-row tiles between them (wave w takes tiles w, w + 4,
+// ...), each staging its own tiles in a wave-private LDS region with the next tile
+// prefetched into registers, and their partial sums meet in LDS at the end in a fixed
+// order (deterministic). Small problems (cfg1: 16 heads of 1024 rows) still fill the
+// chip: one workgroup per 32 keys or rows, four waves each.
+//   dK / dV: lane (g, l) holds key l's K and V dims [g D/2, (g + 1) D/2) as B operands.
+//     S = Q K^T and dP = dO V^T (reduction dim ks for lanes 0-31, D/2 + ks for 32-63);
+//     accumulator element r of lane (g, l) is row 8 (r / 4) + 4 g + r % 4, key l, so
+//     P and dS are directly the B operands of dV^T += dO^T P and dK^T += Q^T dS.
+//   dQ: the same with rows and keys exchanged (S^T = K Q^T, dP^T = V dO^T, lane =
+//     query row with its lse2 / D_i in one register), dQ^T += K^T dS^T.
+// Rows are padded by 4 floats (the forward fp32 kernel's conflict-free pitch).
+// ---------------------------------------------------------------------------------
+constexpr int kM32 = 32;  // keys or rows per workgroup, rows per tile
+
+__device__ inline f32x16 mfma_f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Keeps the compiler from moving LDS accesses across this point. One wave's LDS
+// operations complete in issue order, so a wave-private tile needs no wait or barrier
+// between its writes and the other lanes' reads.
+__device__ inline void wave_lds_order() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+// 32 rows of a [*, D] fp32 tensor held by one wave as f32x4 chunks (chunk j of lane l:
+// row (64 j + l) / (DP / 4), dims 4 x the remainder; rows past `last` re-read it, dims
+// past D are zero), then stored to a wave-private LDS tile of pitch DP + 4.
+template <int DP>
+struct WaveTile {
+  static constexpr int PITCH = DP + 4;
+  static constexpr int CPR = DP / 4;
+  static constexpr int NL = kM32 * CPR / 64;
+  f32x4 x[NL];
+  __device__ inline void load(const float* base, int64_t ss, int r0, int last, int D, int lane) {
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int idx = j * 64 + lane;
+      const int r = idx / CPR;
+      const int c4 = idx - r * CPR;
+      x[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (4 * c4 < D) {  // D % 8 == 0: a chunk is wholly inside or outside
+        x[j] = *reinterpret_cast<const f32x4*>(base + static_cast<int64_t>(min(r0 + r, last)) * ss + 4 * c4);
+      }
+    }
+  }
+  __device__ inline void store(float* t, int lane) const {
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int idx = j * 64 + lane;
+      const int r = idx / CPR;
+      *reinterpret_cast<f32x4*>(t + r * PITCH + 4 * (idx - r * CPR)) = x[j];
+    }
+  }
+};
+
+// dims [g DP/2, (g + 1) DP/2) of one fp32 row (zero past D): the stationary operand
+template <int DP>
+__device__ inline void load_half_row_f32(const float* row, int D, int g, float (&x)[DP / 2]) {
+#pragma unroll
+  for (int c4 = 0; c4 < DP / 2; c4 += 4) {
+    const int d0 = g * (DP / 2) + c4;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (d0 < D) v = *reinterpret_cast<const f32x4*>(row + d0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[c4 + e] = v[e];
+  }
+}
+
+// P and dS of one (row, key) pair from its raw score s = q.k and dP
+template <bool SOFTCAP>
+__device__ inline void f32_pds(const BwdParams& p, float s, float dp, float l2, float di, bool ok,
+                               float& pr, float& ds) {
+  if constexpr (SOFTCAP) {
+    const float t = tanh_fast(s * p.tanh_mul);
+    pr = fast_exp2(fmaf(t, p.cap_mul, -l2));
+    ds = pr * (dp - di) * fmaf(-t, t, 1.0f);
+  } else {
+    pr = fast_exp2(fmaf(s, p.score_mul, -l2));
+    ds = pr * (dp - di);
+  }
+  pr = ok ? pr : 0.0f;
+  ds = ok ? ds : 0.0f;
+}
+
+// Sum the partial accumulators of the four waves in LDS (wave order 0, 1, 2, 3) into
+// wave 0's registers. `red` holds 3 x 64 x NA floats and no tile is in use any more.
+template <int NA>
+__device__ inline void wave_reduce4(float* red, f32x16 (&acc)[NA], int wave, int lane) {
+  __syncthreads();  // every wave is done with its tiles
+  if (wave > 0) {
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[(((wave - 1) * NA + a) * 16 + r) * 64 + lane] = acc[a][r];
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[a][r] += red[((w * NA + a) * 16 + r) * 64 + lane];
+      }
+    }
+  }
+}
+
+// accumulator element (db, r) of lane (g, l32): row dim 32 db + 8 (r / 4) + 4 g + r % 4
+template <int DB>
+__device__ inline void store_acc_row_f32(float* row, const f32x16* acc, float mul, int D, int g) {
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int d0 = 32 * db + 8 * ii + 4 * g;
+      const f32x4 w = {acc[db][4 * ii] * mul, acc[db][4 * ii + 1] * mul, acc[db][4 * ii + 2] * mul,
+                       acc[db][4 * ii + 3] * mul};
+      if (d0 < D) *reinterpret_cast<f32x4*>(row + d0) = w;
+    }
+  }
+}
+
+// dK / dV: one workgroup per CU (its 4 waves hold K, V, dK and dV of 32 keys plus a
+// prefetched tile at head_dim 64; at 128 the tile is loaded when it is needed). dQ: two
+// per CU at head_dim 64.
+template <int DP>
+constexpr int kF32mDqBlocks = DP <= 64 ? 2 : 1;
+template <int DP>
+constexpr bool kF32mDkvPrefetch = DP <= 64;
+
+template <int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads, 1) void bwd_f32m_dkdv_kernel(const BwdParams p) {
+  using T = WaveTile<DP>;
+  constexpr int PITCH = T::PITCH;
+  constexpr int HALF = DP / 2;
+  constexpr int DB = DP / 32;
+  static_assert(3 * 64 * 32 * DB <= 4 * 2 * kM32 * PITCH, "reduction fits in the tiles");
+  __shared__ __attribute__((aligned(16))) float lds[4 * 2 * kM32 * PITCH];
+  __shared__ __attribute__((aligned(16))) float stl[4][2 * kM32];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  float* qt = lds + wave * 2 * kM32 * PITCH;
+  float* dt = qt + kM32 * PITCH;
+  float* st = stl[wave];
+
+  // heaviest key blocks (causal: block 0 sees every row) first, all heads at once
+  const int units = p.B * p.Hkv;
+  const int kb = static_cast<int>(blockIdx.x) / units;
+  const int bh = static_cast<int>(blockIdx.x) - kb * units;
+  const int b = bh / p.Hkv;
+  const int hk = bh - b * p.Hkv;
+  const int D = p.D;
+  const int k0 = kb * kM32;
+  const int key = k0 + l32;
+  const int k_last = min(k0 + kM32, p.Skv) - 1;
+  const int q_lo = p.causal ? max(0, k0 - p.q_offset) : 0;
+  const int q_hi = p.window > 0 ? static_cast<int>(min<int64_t>(
+                                      p.Sq, static_cast<int64_t>(k_last) + p.window - p.q_offset))
+                                : p.Sq;
+  const int j_lo = q_lo / kM32;
+  const int nj = q_hi > q_lo ? (q_hi + kM32 - 1) / kM32 - j_lo : 0;
+  const int n_items = p.ratio * nj;
+
+  const float* qf = reinterpret_cast<const float*>(p.q);
+  const float* dof = reinterpret_cast<const float*>(p.dout);
+  float kreg[HALF], vreg[HALF];
+  {
+    const int kr = min(key, p.Skv - 1);
+    load_half_row_f32<DP>(reinterpret_cast<const float*>(p.k) + b * p.k_sb + hk * p.k_sh +
+                              static_cast<int64_t>(kr) * p.k_ss, D, g, kreg);
+    load_half_row_f32<DP>(reinterpret_cast<const float*>(p.v) + b * p.v_sb + hk * p.v_sh +
+                              static_cast<int64_t>(kr) * p.v_ss, D, g, vreg);
+  }
+  f32x16 acc[2 * DB];  // dK^T blocks, then dV^T blocks
+#pragma unroll
+  for (int a = 0; a < 2 * DB; ++a) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[a][r] = 0.0f;
+  }
+
+  T qn, dn;
+  float statn = 0.0f;
+  // item i: q head hk * ratio + i / nj, row tile j_lo + i % nj
+  auto fetch = [&](int i) {
+    const int hq = hk * p.ratio + i / nj;
+    const int q0 = (j_lo + i % nj) * kM32;
+    qn.load(qf + b * p.q_sb + hq * p.q_sh, p.q_ss, q0, p.Sq - 1, D, lane);
+    dn.load(dof + b * p.do_sb + hq * p.do_sh, p.do_ss, q0, p.Sq - 1, D, lane);
+    // lanes 0-31: lse2 of row q0 + l32, lanes 32-63: D_i (rows < sq_pad)
+    const int64_t ws = (static_cast<int64_t>(b) * p.Hq + hq) * p.sq_pad + q0 + l32;
+    statn = (g == 0 ? p.lse2 : p.di)[ws];
+  };
+  constexpr bool PREFETCH = kF32mDkvPrefetch<DP>;
+  if (PREFETCH && wave < n_items) fetch(wave);
+  for (int i = wave; i < n_items; i += 4) {
+    const int q0 = (j_lo + i % nj) * kM32;
+    if (!PREFETCH) fetch(i);
+    qn.store(qt, lane);
+    dn.store(dt, lane);
+    st[lane] = statn;
+    wave_lds_order();
+    if (PREFETCH && i + 4 < n_items) fetch(i + 4);
+
+    f32x16 s, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = 0.0f;
+      dp[r] = 0.0f;
+    }
+    const float* qrow = qt + l32 * PITCH + g * HALF;
+    const float* drow = dt + l32 * PITCH + g * HALF;
+#pragma unroll
+    for (int ks = 0; ks < HALF; ++ks) {
+      s = mfma_f32(qrow[ks], kreg[ks], s);
+      dp = mfma_f32(drow[ks], vreg[ks], dp);
+    }
+    const int qa0 = p.q_offset + q0;
+    const bool need_mask = q0 + kM32 > p.Sq || k0 + kM32 > p.Skv || (p.causal && qa0 < k0 + kM32 - 1) ||
+                           (p.window > 0 && k0 < qa0 + kM32 - p.window);
+    float pv[16], dsv[16];
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const f32x4 l2 = *reinterpret_cast<const f32x4*>(st + 8 * ii + 4 * g);
+      const f32x4 di = *reinterpret_cast<const f32x4*>(st + kM32 + 8 * ii + 4 * g);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int r = 4 * ii + jj;
+        const int row = 8 * ii + 4 * g + jj;
+        bool ok = true;
+        if (need_mask) {
+          const int qa = qa0 + row;
+          ok = q0 + row < p.Sq && key < p.Skv && (!p.causal || key <= qa) &&
+               (p.window <= 0 || key >= qa - p.window + 1);
+        }
+        f32_pds<SOFTCAP>(p, s[r], dp[r], l2[jj], di[jj], ok, pv[r], dsv[r]);
+      }
+    }
+    // dV^T[d, key] += dO[row, d] P[row, key];  dK^T[d, key] += Q[row, d] dS[row, key]
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int row = 8 * (r >> 2) + 4 * g + (r & 3);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        acc[DB + db] = mfma_f32(dt[row * PITCH + 32 * db + l32], pv[r], acc[DB + db]);
+        acc[db] = mfma_f32(qt[row * PITCH + 32 * db + l32], dsv[r], acc[db]);
+      }
+    }
+    wave_lds_order();
+  }
+
+  wave_reduce4<2 * DB>(lds, acc, wave, lane);
+  if (wave == 0 && key < p.Skv) {
+    float* dkr = reinterpret_cast<float*>(p.dk) + b * p.dk_sb + hk * p.dk_sh + static_cast<int64_t>(key) * p.dk_ss;
+    float* dvr = reinterpret_cast<float*>(p.dv) + b * p.dv_sb + hk * p.dv_sh + static_cast<int64_t>(key) * p.dv_ss;
+    store_acc_row_f32<DB>(dkr, acc, p.scale, D, g);
+    store_acc_row_f32<DB>(dvr, acc + DB, 1.0f, D, g);
+  }
+}
+
+template <int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads, kF32mDqBlocks<DP>) void bwd_f32m_dq_kernel(const BwdParams p) {
+  using T = WaveTile<DP>;
+  constexpr int PITCH = T::PITCH;
+  constexpr int HALF = DP / 2;
+  constexpr int DB = DP / 32;
+  static_assert(3 * 64 * 16 * DB <= 4 * 2 * kM32 * PITCH, "reduction fits in the tiles");
+  __shared__ __attribute__((aligned(16))) float lds[4 * 2 * kM32 * PITCH];
+  __shared__ __attribute__((aligned(16))) float dos[kM32 * PITCH];  // the 32 rows' dO, shared
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  float* kt = lds + wave * 2 * kM32 * PITCH;
+  float* vt = kt + kM32 * PITCH;
+
+  // heaviest row blocks (causal: the last) first, all heads at once
+  const int units = p.B * p.Hq;
+  const int n_rb = (p.Sq + kM32 - 1) / kM32;
+  const int jb = static_cast<int>(blockIdx.x) / units;
+  const int bh = static_cast<int>(blockIdx.x) - jb * units;
+  const int rb = p.causal ? n_rb - 1 - jb : jb;
+  const int b = bh / p.Hq;
+  const int h = bh - b * p.Hq;
+  const int hk = h / p.ratio;
+  const int D = p.D;
+  const int q0 = rb * kM32;
+  const int qrow = q0 + l32;
+  const int qa = p.q_offset + qrow;
+  const int qa0 = p.q_offset + q0;
+  const int kv_lo = p.window > 0 ? max(0, qa0 - p.window + 1) : 0;
+  const int kv_hi = p.causal ? min(p.Skv, p.q_offset + min(q0 + kM32, p.Sq)) : p.Skv;
+  const int t_lo = kv_lo / kM32;
+  const int nt = kv_hi > kv_lo ? (kv_hi + kM32 - 1) / kM32 - t_lo : 0;
+
+  // Q^T operand in registers; dO^T (the same for all four waves) from LDS
+  float qreg[HALF];
+  load_half_row_f32<DP>(reinterpret_cast<const float*>(p.q) + b * p.q_sb + h * p.q_sh +
+                            static_cast<int64_t>(min(qrow, p.Sq - 1)) * p.q_ss, D, g, qreg);
+  {
+    const float* dob = reinterpret_cast<const float*>(p.dout) + b * p.do_sb + h * p.do_sh;
+    for (int idx = tid; idx < kM32 * T::CPR; idx += kThreads) {
+      const int r = idx / T::CPR;
+      const int c4 = idx - r * T::CPR;
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      if (4 * c4 < D) {
+        x = *reinterpret_cast<const f32x4*>(dob + static_cast<int64_t>(min(q0 + r, p.Sq - 1)) * p.do_ss + 4 * c4);
+      }
+      *reinterpret_cast<f32x4*>(dos + r * PITCH + 4 * c4) = x;
+    }
+  }
+  const int64_t ws = static_cast<int64_t>(bh) * p.sq_pad + qrow;  // qrow < sq_pad
+  const float l2 = p.lse2[ws];
+  const float di = p.di[ws];
+  const float* kb = reinterpret_cast<const float*>(p.k) + b * p.k_sb + hk * p.k_sh;
+  const float* vb = reinterpret_cast<const float*>(p.v) + b * p.v_sb + hk * p.v_sh;
+
+  f32x16 acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.0f;
+  }
+  T kn, vn;
+  if (wave < nt) {
+    kn.load(kb, p.k_ss, (t_lo + wave) * kM32, p.Skv - 1, D, lane);
+    vn.load(vb, p.v_ss, (t_lo + wave) * kM32, p.Skv - 1, D, lane);
+  }
+  __syncthreads();  // dO tile written
+  for (int t = wave; t < nt; t += 4) {
+    const int k0 = (t_lo + t) * kM32;
+    kn.store(kt, lane);
+    vn.store(vt, lane);
+    wave_lds_order();
+    if (t + 4 < nt) {
+      kn.load(kb, p.k_ss, k0 + 4 * kM32, p.Skv - 1, D, lane);
+      vn.load(vb, p.v_ss, k0 + 4 * kM32, p.Skv - 1, D, lane);
+    }
+
+    f32x16 s, dp;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = 0.0f;
+      dp[r] = 0.0f;
+    }
+    const float* krow = kt + l32 * PITCH + g * HALF;
+    const float* vrow = vt + l32 * PITCH + g * HALF;
+    const float* dorow = dos + l32 * PITCH + g * HALF;
+#pragma unroll
+    for (int ks = 0; ks < HALF; ++ks) {
+      s = mfma_f32(krow[ks], qreg[ks], s);
+      dp = mfma_f32(vrow[ks], dorow[ks], dp);
+    }
+    const bool need_mask = k0 + kM32 > p.Skv || q0 + kM32 > p.Sq || (p.causal && k0 + kM32 - 1 > qa0) ||
+                           (p.window > 0 && k0 < qa0 + kM32 - p.window);
+    float dsv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      bool ok = true;
+      if (need_mask) {
+        const int kk = k0 + 8 * (r >> 2) + 4 * g + (r & 3);
+        ok = kk < p.Skv && qrow < p.Sq && (!p.causal || kk <= qa) && (p.window <= 0 || kk >= qa - p.window + 1);
+      }
+      float pr;
+      f32_pds<SOFTCAP>(p, s[r], dp[r], l2, di, ok, pr, dsv[r]);
+    }
+    // dQ^T[d, row] += K[key, d] dS[row, key]
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] = mfma_f32(kt[kk * PITCH + 32 * db + l32], dsv[r], acc[db]);
+    }
+    wave_lds_order();
+  }
+
+  wave_reduce4<DB>(lds, acc, wave, lane);
+  if (wave == 0 && qrow < p.Sq) {
+    float* dqr = reinterpret_cast<float*>(p.dq) + b * p.dq_sb + h * p.dq_sh + static_cast<int64_t>(qrow) * p.dq_ss;
+    store_acc_row_f32<DB>(dqr, acc, p.scale, D, g);
+  }
+}
+
+template <int DP, bool SOFTCAP>
+void launch_f32m_dp(const BwdParams& p, hipStream_t s) {
+  const int grid_dkv = p.B * p.Hkv * ((p.Skv + kM32 - 1) / kM32);
+  const int grid_dq = p.B * p.Hq * ((p.Sq + kM32 - 1) / kM32);
+  if (grid_dkv > 0) {
+    hipLaunchKernelGGL((bwd_f32m_dkdv_kernel<DP, SOFTCAP>), dim3(grid_dkv), dim3(kThreads), 0, s, p);
+  }
+  hipLaunchKernelGGL((bwd_f32m_dq_kernel<DP, SOFTCAP>), dim3(grid_dq), dim3(kThreads), 0, s, p);
+}
+
 void launch_f32(const BwdParams& p, bool softcap, int grid_pre, hipStream_t s) {
   hipLaunchKernelGGL((bwd_pre_kernel<F32Tag>), dim3(grid_pre), dim3(kThreads), 0, s, p);
   if (p.D <= 64) {
-    softcap ? launch_f32_dp<64, true>(p, s) : launch_f32_dp<64, false>(p, s);
+    softcap ? launch_f32m_dp<64, true>(p, s) : launch_f32m_dp<64, false>(p, s);
   } else if (p.D <= 128) {
-    softcap ? launch_f32_dp<128, true>(p, s) : launch_f32_dp<128, false>(p, s);
+    softcap ? launch_f32m_dp<128, true>(p, s) : launch_f32m_dp<128, false>(p, s);
   } else {
     softcap ? launch_f32_dp<256, true>(p, s) : launch_f32_dp<256, false>(p, s);
   }

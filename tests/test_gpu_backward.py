@@ -98,6 +98,16 @@ CASES = [
     ("fp32_d256_causal", 1, 2, 2, 97, 97, 256, 0, {"causal": True}, F32),
     ("fp32_q_offset", 1, 2, 2, 40, 180, 64, 140, {"causal": True, "softcap": 15.0}, F32),
     ("fp32_single", 1, 1, 1, 1, 1, 64, 0, {}, F32),
+    # fp32 MFMA kernels (head_dim <= 128): GQA + window + softcap over many tiles per
+    # wave, ragged ends, q_offset with a window, negative scale, MQA at head_dim 128
+    ("fp32_d64_gqa_window_softcap", 2, 8, 2, 300, 300, 64, 0,
+     {"causal": True, "sliding_window": 100, "softcap": 30.0}, F32),
+    ("fp32_d128_causal_ragged", 1, 3, 3, 289, 289, 128, 0, {"causal": True}, F32),
+    ("fp32_d96_qoffset_window", 1, 2, 1, 70, 250, 96, 180,
+     {"causal": True, "sliding_window": 64}, F32),
+    ("fp32_d128_mqa_window_noncausal", 1, 4, 1, 150, 203, 128, 0, {"sliding_window": 45}, F32),
+    ("fp32_negative_scale", 1, 2, 2, 150, 150, 64, 0, {"causal": True, "scale": -0.2}, F32),
+    ("fp32_d16_noncausal", 2, 2, 2, 40, 67, 16, 0, {}, F32),
 ]
 
 
