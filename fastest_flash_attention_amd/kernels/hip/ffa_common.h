@@ -97,6 +97,10 @@ __device__ inline float tanh_approx(float y) {
 
 // tanh(y) = 1 - 2 / (1 + e^{2y}), given x = 2y * log2(e): exp2, add, rcp, fma. It
 // saturates to -1 / +1 for large |y| (e^{2y} = 0 / inf); |error| ~ 1e-7 absolute.
+__device__ inline float tanh_fast(float x) {
+  return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + fast_exp2(x)), 1.0f);
+}
+
 // Positions (q_offset + row, key index) are int32 inside the kernels; the C ABI keeps
 // |q_offset|, q_offset + S_q and S_kv at most kMaxPos.
 constexpr int kMaxPos = 0x1fffffff;
@@ -109,10 +113,6 @@ __host__ __device__ inline int clamp_window(int window, int q_offset, int seqlen
   if (window <= 0) return 0;
   const int64_t lim = static_cast<int64_t>(q_offset) + seqlen_q + 1;
   return static_cast<int>(window < lim ? window : (lim < 1 ? 1 : lim));
-}
-
-__device__ inline float tanh_fast(float x) {
-  return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + fast_exp2(x)), 1.0f);
 }
 
 // Eight consecutive 16-bit elements row[d0 .. d0+7] as one 128-bit value, zero

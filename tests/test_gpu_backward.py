@@ -141,12 +141,14 @@ def test_backward_parity(case):
     _check(dv, rv, dt, f"{name} dv")
 
 
-def test_backward_deterministic():
-    """No atomics: two calls give bit-identical gradients."""
+@pytest.mark.parametrize("dt", [BF16, F32], ids=["bf16", "fp32"])
+def test_backward_deterministic(dt):
+    """No atomics: two calls give bit-identical gradients (fp32: the four waves' partial
+    sums of a block meet in a fixed order)."""
     require_gpu()
     B, H, S, D = 2, 4, 300, 128
-    q, k, v, do = (seeded((B, H, S, D), BF16, s).cuda() for s in (11, 12, 13, 14))
-    say("backward determinism")
+    q, k, v, do = (seeded((B, H, S, D), dt, s).cuda() for s in (11, 12, 13, 14))
+    say(f"backward determinism {dt}")
     o, lse = ffa.fastest_flash_attn_forward(q, k, v, causal=True, return_lse=True)
     a = ffa.fastest_flash_attn_backward(do, q, k, v, o, lse, causal=True)
     b = ffa.fastest_flash_attn_backward(do, q, k, v, o, lse, causal=True)
