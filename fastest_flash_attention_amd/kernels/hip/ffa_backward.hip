@@ -429,6 +429,10 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
       dkacc[db][r] = 0.0f;
       dvacc[db][r] = 0.0f;
     }
+    if constexpr (kBwdMinBlocks<DP> == 1) {
+      pin_agpr(dkacc[db]);
+      pin_agpr(dvacc[db]);
+    }
   }
 
   if (nit > 0) issue(0);
@@ -528,6 +532,13 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
         const u32x4 aq = tr_operand<DP>(ql + 16 * cc * DP, t_lo, t_hi, db);
         dvacc[db] = E::mfma32(ado, bp, dvacc[db]);
         dkacc[db] = E::mfma32(aq, bs, dkacc[db]);
+      }
+    }
+    if constexpr (kBwdMinBlocks<DP> == 1) {
+#pragma unroll
+      for (int db = 0; db < S::DB; ++db) {
+        pin_agpr(dkacc[db]);
+        pin_agpr(dvacc[db]);
       }
     }
   }
@@ -644,6 +655,7 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
   for (int db = 0; db < S::DB; ++db) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dqacc[db][r] = 0.0f;
+    if constexpr (kBwdMinBlocks<DP> == 1) pin_agpr(dqacc[db]);
   }
 
   if (nt > 0) issue(t_begin, 0);
@@ -728,6 +740,10 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
         const u32x4 ak = tr_operand<DP>(kl + 16 * cc * DP, t_lo, t_hi, db);
         dqacc[db] = E::mfma32(ak, bs, dqacc[db]);
       }
+    }
+    if constexpr (kBwdMinBlocks<DP> == 1) {
+#pragma unroll
+      for (int db = 0; db < S::DB; ++db) pin_agpr(dqacc[db]);
     }
   }
 
@@ -1151,6 +1167,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_f32m_dkdv_kernel(const BwdPar
   for (int a = 0; a < 2 * DB; ++a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[a][r] = 0.0f;
+    pin_agpr(acc[a]);
   }
 
   T qn, dn;
@@ -1220,6 +1237,8 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_f32m_dkdv_kernel(const BwdPar
         acc[db] = mfma_f32(qt[row * PITCH + 32 * db + l32], dsv[r], acc[db]);
       }
     }
+#pragma unroll
+    for (int a = 0; a < 2 * DB; ++a) pin_agpr(acc[a]);
     wave_lds_order();
   }
 
@@ -1295,6 +1314,7 @@ __global__ __launch_bounds__(kThreads, kF32mDqBlocks<DP>) void bwd_f32m_dq_kerne
   for (int db = 0; db < DB; ++db) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.0f;
+    if constexpr (kF32mDqBlocks<DP> == 1) pin_agpr(acc[db]);
   }
   T kn, vn;
   if (wave < nt) {
@@ -1345,6 +1365,10 @@ __global__ __launch_bounds__(kThreads, kF32mDqBlocks<DP>) void bwd_f32m_dq_kerne
       const int kk = 8 * (r >> 2) + 4 * g + (r & 3);
 #pragma unroll
       for (int db = 0; db < DB; ++db) acc[db] = mfma_f32(kt[kk * PITCH + 32 * db + l32], dsv[r], acc[db]);
+    }
+    if constexpr (kF32mDqBlocks<DP> == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) pin_agpr(acc[db]);
     }
     wave_lds_order();
   }

@@ -101,6 +101,13 @@ __device__ inline float tanh_fast(float x) {
   return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + fast_exp2(x)), 1.0f);
 }
 
+// Ties an MFMA accumulator to the accumulation registers (AGPRs) at this point; emits
+// no instruction. Kernels that run one workgroup per CU (512 registers per lane) call it
+// on their loop-carried accumulators: left alone, the register allocator keeps them in
+// VGPRs and copies them into AGPRs and back around the MFMAs (hundreds of
+// v_accvgpr_write / read per tile), or spills.
+__device__ inline void pin_agpr(f32x16& acc) { asm volatile("" : "+a"(acc)); }
+
 // Positions (q_offset + row, key index) are int32 inside the kernels; the C ABI keeps
 // |q_offset|, q_offset + S_q and S_kv at most kMaxPos.
 constexpr int kMaxPos = 0x1fffffff;

@@ -24,8 +24,6 @@ from fastest_flash_attention_amd.kernels.hip import build
 EXCEPTIONS = {
     # head_dim 192 with softcap: the tanh work of 32-key tiles at 256 VGPRs
     r"prefill_kernel<.*, 192, 32, true>": 16,
-    # head_dim 256 dK/dV: 2 x 32 keys x 256 dims of fp32 accumulators per wave
-    r"bwd_dkdv_kernel<.*, 256, (true|false)>": 512,
 }
 
 
