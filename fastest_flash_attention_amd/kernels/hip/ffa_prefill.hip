@@ -307,6 +307,28 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     for (int nb = 0; nb < S::NB; ++nb) {
       a_cur[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd[0] + nb * 32 * DP);
     }
+    // head_dim 192 (32-key tiles, one 32-key block): the 12 k-steps would form one chain
+    // of dependent MFMAs, so even and odd k-steps go to two accumulators summed at the
+    // end (+2.3 % at cfg5 on MI355X; with softcap it spills, and at 256 it is slower)
+    if constexpr (DP == 192 && !SOFTCAP) {
+      f32x16 s_odd;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_odd[r] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < S::KS; ++ks) {
+        if (ks + 1 < S::KS) a_nxt[0] = *reinterpret_cast<const u32x4*>(kl + k_rd[ks + 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks & 1) {
+          s_odd = E::mfma32(a_cur[0], qreg[ks], s_odd);
+        } else {
+          sacc[0] = E::mfma32(a_cur[0], qreg[ks], sacc[0]);
+        }
+        a_cur[0] = a_nxt[0];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[0][r] += s_odd[r];
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
       if (ks + 1 < S::KS) {
