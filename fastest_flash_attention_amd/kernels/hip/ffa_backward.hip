@@ -999,46 +999,6 @@ void launch_f32_dp(const BwdParams& p, hipStream_t s) {
 // ---------------------------------------------------------------------------------
 constexpr int kM32 = 32;  // keys or rows per workgroup, rows per tile
 
-__device__ inline f32x16 mfma_f32(float a, float b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
-
-// Keeps the compiler from moving LDS accesses across this point. One wave's LDS
-// operations complete in issue order, so a wave-private tile needs no wait or barrier
-// between its writes and the other lanes' reads.
-__device__ inline void wave_lds_order() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
-
-// 32 rows of a [*, D] fp32 tensor held by one wave as f32x4 chunks (chunk j of lane l:
-// row (64 j + l) / (DP / 4), dims 4 x the remainder; rows past `last` re-read it, dims
-// past D are zero), then stored to a wave-private LDS tile of pitch DP + 4.
-template <int DP>
-struct WaveTile {
-  static constexpr int PITCH = DP + 4;
-  static constexpr int CPR = DP / 4;
-  static constexpr int NL = kM32 * CPR / 64;
-  f32x4 x[NL];
-  __device__ inline void load(const float* base, int64_t ss, int r0, int last, int D, int lane) {
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-      const int idx = j * 64 + lane;
-      const int r = idx / CPR;
-      const int c4 = idx - r * CPR;
-      x[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (4 * c4 < D) {  // D % 8 == 0: a chunk is wholly inside or outside
-        x[j] = *reinterpret_cast<const f32x4*>(base + static_cast<int64_t>(min(r0 + r, last)) * ss + 4 * c4);
-      }
-    }
-  }
-  __device__ inline void store(float* t, int lane) const {
-#pragma unroll
-    for (int j = 0; j < NL; ++j) {
-      const int idx = j * 64 + lane;
-      const int r = idx / CPR;
-      *reinterpret_cast<f32x4*>(t + r * PITCH + 4 * (idx - r * CPR)) = x[j];
-    }
-  }
-};
-
 // dims [g DP/2, (g + 1) DP/2) of one fp32 row (zero past D): the stationary operand
 template <int DP>
 __device__ inline void load_half_row_f32(const float* row, int D, int g, float (&x)[DP / 2]) {
@@ -1118,7 +1078,7 @@ constexpr bool kF32mDkvPrefetch = DP <= 64;
 
 template <int DP, bool SOFTCAP>
 __global__ __launch_bounds__(kThreads, 1) void bwd_f32m_dkdv_kernel(const BwdParams p) {
-  using T = WaveTile<DP>;
+  using T = F32WaveTile<DP>;
   constexpr int PITCH = T::PITCH;
   constexpr int HALF = DP / 2;
   constexpr int DB = DP / 32;
@@ -1253,7 +1213,7 @@ __global__ __launch_bounds__(kThreads, 1) void bwd_f32m_dkdv_kernel(const BwdPar
 
 template <int DP, bool SOFTCAP>
 __global__ __launch_bounds__(kThreads, kF32mDqBlocks<DP>) void bwd_f32m_dq_kernel(const BwdParams p) {
-  using T = WaveTile<DP>;
+  using T = F32WaveTile<DP>;
   constexpr int PITCH = T::PITCH;
   constexpr int HALF = DP / 2;
   constexpr int DB = DP / 32;

@@ -108,6 +108,50 @@ __device__ inline float tanh_fast(float x) {
 // v_accvgpr_write / read per tile), or spills.
 __device__ inline void pin_agpr(f32x16& acc) { asm volatile("" : "+a"(acc)); }
 
+// fp32 x fp32 -> fp32 MFMA, 32x32 output, k = 2: lane (g, l) supplies A[l][g] and
+// B[g][l]; accumulator element r of lane (g, l) is C[8 (r / 4) + 4 g + r % 4][l].
+__device__ inline f32x16 mfma_f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Keeps the compiler from moving LDS accesses across this point. One wave's LDS
+// operations complete in issue order, so a wave-private tile needs no wait or barrier
+// between its writes and the other lanes' reads.
+__device__ inline void wave_lds_order() { __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront"); }
+
+// 32 rows of a [*, D] fp32 tensor held by one wave as f32x4 chunks (chunk j of lane l:
+// row (64 j + l) / (DP / 4), dims 4 x the remainder; rows past `last` re-read it, dims
+// past D are zero), then stored to a wave-private LDS tile of pitch DP + 4 (rows
+// 16-byte aligned; 32 rows read at one dim offset hit distinct banks).
+template <int DP>
+struct F32WaveTile {
+  static constexpr int ROWS = 32;
+  static constexpr int PITCH = DP + 4;
+  static constexpr int CPR = DP / 4;
+  static constexpr int NL = ROWS * CPR / 64;
+  f32x4 x[NL];
+  __device__ inline void load(const float* base, int64_t ss, int r0, int last, int D, int lane) {
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int idx = j * 64 + lane;
+      const int r = idx / CPR;
+      const int c4 = idx - r * CPR;
+      x[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (4 * c4 < D) {  // D % 8 == 0: a chunk is wholly inside or outside
+        x[j] = *reinterpret_cast<const f32x4*>(base + static_cast<int64_t>(min(r0 + r, last)) * ss + 4 * c4);
+      }
+    }
+  }
+  __device__ inline void store(float* t, int lane) const {
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int idx = j * 64 + lane;
+      const int r = idx / CPR;
+      *reinterpret_cast<f32x4*>(t + r * PITCH + 4 * (idx - r * CPR)) = x[j];
+    }
+  }
+};
+
 // Positions (q_offset + row, key index) are int32 inside the kernels; the C ABI keeps
 // |q_offset|, q_offset + S_q and S_kv at most kMaxPos.
 constexpr int kMaxPos = 0x1fffffff;

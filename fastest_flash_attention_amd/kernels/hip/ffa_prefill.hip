@@ -685,10 +685,6 @@ void launch_tag(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
 // ---------------------------------------------------------------------------------
 constexpr int kF32BN = 32;
 
-__device__ inline f32x16 mfma_f32(float a, float b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
-
 template <int DP, bool SOFTCAP>
 __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillParams p) {
   constexpr int PITCH = DP + 4;
@@ -863,8 +859,242 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillP
   }
 }
 
+// ---------------------------------------------------------------------------------
+// fp32 inputs on grids too small for the kernel above (fewer than 2048 128-row
+// workgroups; cfg1 has 128): one workgroup per 32 query rows, and its 4 waves
+// split the key range (wave w takes 32-key tiles w, w + 4, ...), each staging its own
+// tiles in a wave-private LDS region with the next one prefetched into registers, and
+// each keeping its own running max, sum and O^T for the 32 rows (the per-tile math is
+// the kernel above's). The four partial states meet in LDS at the end and wave 0
+// merges them in a fixed order: O = sum_w 2^((m_w - m) c) O_w / sum_w 2^((m_w - m) c) l_w.
+// ---------------------------------------------------------------------------------
+template <int DP>
+constexpr int kF32SplitBlocks = DP <= 64 ? 2 : 1;
+
+template <int DP, bool SOFTCAP>
+__global__ __launch_bounds__(kThreads, kF32SplitBlocks<DP>) void prefill_f32_split_kernel(const PrefillParams p) {
+  using T = F32WaveTile<DP>;
+  constexpr int PITCH = T::PITCH;
+  constexpr int HALF = DP / 2;
+  constexpr int DB = DP / 32;
+  constexpr int NE = 16 * DB + 2;  // floats per lane in the merge: O^T, m, l
+  static_assert(3 * NE * 64 <= 4 * 2 * kF32BN * PITCH, "merge fits in the tiles");
+  __shared__ __attribute__((aligned(16))) float lds[4 * 2 * kF32BN * PITCH];
+  const float* qf = reinterpret_cast<const float*>(p.q);
+  const float* kf = reinterpret_cast<const float*>(p.k);
+  const float* vf = reinterpret_cast<const float*>(p.v);
+  float* of = reinterpret_cast<float*>(p.o);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  float* kt = lds + wave * 2 * kF32BN * PITCH;
+  float* vt = kt + kF32BN * PITCH;
+
+  // heaviest row blocks (causal: the last) first, all heads at once
+  const int units = p.B * p.Hq;
+  const int n_rb = (p.Sq + kF32BN - 1) / kF32BN;
+  const int jb = static_cast<int>(blockIdx.x) / units;
+  const int bh = static_cast<int>(blockIdx.x) - jb * units;
+  const int rb = p.causal ? n_rb - 1 - jb : jb;
+  const int b = bh / p.Hq;
+  const int h = bh - b * p.Hq;
+  const int hk = h / p.ratio;
+  const int D = p.D;
+  const int Skv = p.Skv;
+
+  const int q0 = rb * kF32BN;
+  const int qrow = q0 + l32;
+  const int qa = p.q_offset + qrow;
+  const int qa0 = p.q_offset + q0;
+  const int ql_abs = p.q_offset + min(q0 + kF32BN, p.Sq) - 1;
+  const int kv_lo = p.window > 0 ? max(0, qa0 - p.window + 1) : 0;
+  const int kv_hi = p.causal ? min(Skv, ql_abs + 1) : Skv;
+  const int t_lo = kv_lo / kF32BN;
+  const int nt = kv_hi > kv_lo ? (kv_hi + kF32BN - 1) / kF32BN - t_lo : 0;
+  const uint64_t* kmask_row =
+      p.kmask != nullptr ? p.kmask + static_cast<int64_t>(min(qrow, p.Sq - 1) / p.ref_bq) * p.kmask_words
+                         : nullptr;
+  const float c = SOFTCAP ? 1.0f : p.score_mul;
+  const float thresh = SOFTCAP ? kRescaleThresh : kRescaleThresh / p.score_mul;
+
+  // Q^T operand: lane holds row qrow, dims g*HALF .. g*HALF + HALF - 1 (zero past D)
+  float qreg[HALF];
+  {
+    const float* qr = qf + b * p.q_sb + h * p.q_sh + static_cast<int64_t>(min(qrow, p.Sq - 1)) * p.q_ss;
+#pragma unroll
+    for (int c4 = 0; c4 < HALF; c4 += 4) {
+      const int d0 = g * HALF + c4;
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (d0 < D) v = *reinterpret_cast<const f32x4*>(qr + d0);  // D % 8 == 0
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qreg[c4 + e] = p.q_neg ? -v[e] : v[e];  // negative scale
+    }
+  }
+  f32x16 oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
+  }
+  float m_run = kNegInf;
+  float l_run = 0.0f;
+  const float* kbase = kf + b * p.k_sb + hk * p.k_sh;
+  const float* vbase = vf + b * p.v_sb + hk * p.v_sh;
+
+  T kn, vn;
+  if (wave < nt) {
+    kn.load(kbase, p.k_ss, (t_lo + wave) * kF32BN, Skv - 1, D, lane);
+    vn.load(vbase, p.v_ss, (t_lo + wave) * kF32BN, Skv - 1, D, lane);
+  }
+  for (int t = wave; t < nt; t += 4) {
+    const int kt0 = (t_lo + t) * kF32BN;
+    kn.store(kt, lane);
+    vn.store(vt, lane);
+    wave_lds_order();
+    if (t + 4 < nt) {
+      kn.load(kbase, p.k_ss, kt0 + 4 * kF32BN, Skv - 1, D, lane);
+      vn.load(vbase, p.v_ss, kt0 + 4 * kF32BN, Skv - 1, D, lane);
+    }
+
+    f32x16 sacc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+    const float* krow = kt + l32 * PITCH + g * HALF;
+#pragma unroll
+    for (int ks = 0; ks < HALF; ++ks) sacc = mfma_f32(krow[ks], qreg[ks], sacc);
+
+    if constexpr (SOFTCAP) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = p.cap_mul * tanh_approx(sacc[r] * p.score_mul);
+    }
+    const bool need_mask = (kt0 + kF32BN > Skv) || (p.causal && kt0 + kF32BN - 1 > qa0) ||
+                           (p.window > 0 && kt0 < ql_abs - p.window + 1) || p.kmask != nullptr;
+    if (need_mask) {
+      const uint64_t kbits =
+          p.kmask != nullptr ? kmask_row[kt0 >> 6] >> (kt0 & 63) : ~uint64_t{0};
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int off = 8 * (r >> 2) + 4 * g + (r & 3);
+        const int key = kt0 + off;
+        const bool ok = key < Skv && (!p.causal || key <= qa) &&
+                        (p.window <= 0 || key >= qa - p.window + 1) && ((kbits >> off) & 1u);
+        sacc[r] = ok ? sacc[r] : kNegInf;
+      }
+    }
+    float mt = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[r]);
+    mt = wave_pair_max(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const bool need = m_new > m_run + thresh;
+    if (__any(need)) {
+      const float alpha = need ? fast_exp2((m_run - m_new) * c) : 1.0f;
+      m_run = need ? m_new : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      }
+    }
+    const float mc = (m_run == kNegInf) ? 0.0f : m_run * c;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = fast_exp2(fmaf(sacc[r], c, -mc));
+      l_run += sacc[r];
+    }
+    // O^T[d, q] += sum over keys 8ii + 4g + jj of V[key][d] P[q][key]
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = 8 * (r >> 2) + 4 * g + (r & 3);
+        oacc[db] = mfma_f32(vt[key * PITCH + 32 * db + l32], sacc[r], oacc[db]);
+      }
+    }
+    wave_lds_order();
+  }
+
+  // merge: waves 1-3 leave (O^T, m, l) in LDS, wave 0 combines them with its own
+  const float l_w = wave_pair_sum(l_run);
+  __syncthreads();  // every wave is done with its tiles
+  if (wave > 0) {
+    float* dst = lds + (wave - 1) * NE * 64 + lane;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dst[(16 * db + r) * 64] = oacc[db][r];
+    }
+    dst[(16 * DB) * 64] = m_run;
+    dst[(16 * DB + 1) * 64] = l_w;
+  }
+  __syncthreads();
+  if (wave != 0 || qrow >= p.Sq) return;
+  float mw[4], lw[4];
+  mw[0] = m_run;
+  lw[0] = l_w;
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    mw[w] = lds[((w - 1) * NE + 16 * DB) * 64 + lane];
+    lw[w] = lds[((w - 1) * NE + 16 * DB + 1) * 64 + lane];
+  }
+  const float m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
+  float sc[4];
+  float l_tot = 0.0f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    sc[w] = mw[w] == kNegInf ? 0.0f : fast_exp2((mw[w] - m) * c);  // a wave with no key: 0
+    l_tot = fmaf(sc[w], lw[w], l_tot);
+  }
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float o = sc[0] * oacc[db][r];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) o = fmaf(sc[w], lds[((w - 1) * NE + 16 * db + r) * 64 + lane], o);
+      oacc[db][r] = o;
+    }
+  }
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  float* orow = of + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int d0 = 32 * db + 8 * ii + 4 * g;
+      const f32x4 w = {oacc[db][4 * ii + 0] * inv, oacc[db][4 * ii + 1] * inv,
+                       oacc[db][4 * ii + 2] * inv, oacc[db][4 * ii + 3] * inv};
+      if (d0 < D) *reinterpret_cast<f32x4*>(orow + d0) = w;
+    }
+  }
+  if (p.lse != nullptr && g == 0) {
+    const float lse = l_tot > 0.0f ? (m * c + fast_log2(l_tot)) * kLn2 : masked_row_lse(p, qrow);
+    p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(qrow) * p.l_ss] = lse;
+  }
+}
+
+// Workgroups of the 128-row fp32 kernel below which the split kernel runs instead
+// (fewer than eight per CU). Measured on MI355X: 2.4x at cfg1 (128 workgroups), 1.7x
+// at 512, 1.4x at 1024; at 4096 and more the two are within -9 % .. +4 % of each other.
+constexpr int64_t kF32SplitBelow = 2048;
+
 template <int DP>
 void launch_f32_dp(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
+  if constexpr (DP <= 128) {
+    if (grid < kF32SplitBelow) {
+      const int grid_s = p.B * p.Hq * ((p.Sq + kF32BN - 1) / kF32BN);  // <= 4 * grid
+      if (softcap) {
+        hipLaunchKernelGGL((prefill_f32_split_kernel<DP, true>), dim3(grid_s), dim3(kThreads), 0, s, p);
+      } else {
+        hipLaunchKernelGGL((prefill_f32_split_kernel<DP, false>), dim3(grid_s), dim3(kThreads), 0, s, p);
+      }
+      return;
+    }
+  }
   if (softcap) {
     hipLaunchKernelGGL((prefill_f32_kernel<DP, true>), dim3(grid), dim3(kThreads), 0, s, p);
   } else {

@@ -27,6 +27,10 @@ BM_CASES = [
     ("sparse_gqa_d192", 1, 4, 2, 100, 100, 192, 8, 0.5, {"num_kv_heads": 2}, BF16),
     ("sparse_fp16_small_blocks", 1, 2, 2, 40, 40, 32, 4, 0.5, {"causal": True}, F16),
     ("sparse_rect", 1, 2, 2, 48, 150, 64, 16, 0.6, {}, BF16),
+    # fp32 inputs (the split fp32 kernel at these grid sizes)
+    ("sparse_fp32_causal", 1, 4, 4, 200, 200, 64, 16, 0.6, {"causal": True}, torch.float32),
+    ("sparse_fp32_gqa_window_softcap", 1, 4, 2, 150, 170, 128, 32, 0.7,
+     {"sliding_window": 60, "softcap": 25.0, "num_kv_heads": 2}, torch.float32),
 ]
 
 

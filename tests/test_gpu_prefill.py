@@ -257,9 +257,20 @@ def test_full_size_sampled_heads(cfg):
 
 
 # fp32 inputs: computed in fp32 (fp32 MFMA), as the reference computes them; the
-# tolerance is the north-star one, the fp32 path lands far inside it.
+# tolerance is the north-star one, the fp32 path lands far inside it. Grids of fewer
+# than 2048 128-row workgroups (all but the two "classic" cases, which have exactly
+# 2048, and head_dim > 128) run the split kernel, whose four waves share a row block's
+# keys; "long_kv" gives each wave many tiles, "few_tiles" leaves some waves none.
 F32_CASES = [
     ("cfg1_mha_fp32", 2, 8, 8, 1024, 1024, 64, {"causal": True, "block_size": 64}),
+    ("fp32_classic_grid_causal", 2, 32, 32, 4096, 4096, 32, {"causal": True}),
+    ("fp32_classic_grid_gqa_window", 1, 64, 16, 4096, 4096, 32,
+     {"causal": True, "sliding_window": 300, "num_kv_heads": 16}),
+    ("fp32_split_grid_512_gqa_window", 1, 32, 8, 2048, 2048, 64,
+     {"causal": True, "sliding_window": 300, "num_kv_heads": 8}),
+    ("fp32_split_long_kv", 1, 4, 4, 5, 3000, 64, {}),
+    ("fp32_split_long_kv_causal_topleft", 1, 2, 2, 70, 2500, 128, {"causal": True}),
+    ("fp32_split_few_tiles", 2, 3, 3, 40, 40, 64, {"causal": True}),
     ("fp32_window_softcap_gqa", 1, 4, 2, 200, 200, 128, {"causal": True, "sliding_window": 50,
                                                          "softcap": 30.0, "num_kv_heads": 2}),
     ("fp32_d32_noncausal_rect", 2, 2, 2, 70, 130, 32, {}),
