@@ -381,15 +381,34 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       }
       rd_k(0);
     }
+    // Softcap: the scores are kept as r = 1 / (1 + e^{2y}), tanh(y) = 1 - 2r, so the
+    // exponent c tanh(y) - m c = c (1 - 2r) - m c is one FMA of r (the FMA that would
+    // form tanh from r is folded into it). A masked element is r = +inf (tanh = -inf).
     if constexpr (SOFTCAP) {
 #pragma unroll
       for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          sacc[nb][r] = tanh_fast(sacc[nb][r] * tanh_mul);
+          sacc[nb][r] = __builtin_amdgcn_rcpf(1.0f + fast_exp2(sacc[nb][r] * tanh_mul));
         }
       }
     }
+    constexpr float kMasked = SOFTCAP ? __builtin_inff() : kNegInf;
+    // the tile's row max in score units (softcap: 1 - 2 min r)
+    auto tile_max = [&]() __attribute__((always_inline)) {
+      float mt = SOFTCAP ? __builtin_inff() : kNegInf;
+#pragma unroll
+      for (int nb2 = 0; nb2 < S::NB; ++nb2) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = SOFTCAP ? fminf(mt, sacc[nb2][r]) : fmaxf(mt, sacc[nb2][r]);
+      }
+      if constexpr (SOFTCAP) {
+        mt = -wave_pair_max(-mt);
+        return fmaf(-2.0f, mt, 1.0f);
+      } else {
+        return wave_pair_max(mt);
+      }
+    };
     const bool need_mask = MAYMASK && ((kt0 + BN > Skv) || (p.causal && kt0 + BN - 1 > qw0_abs) ||
                                        (p.window > 0 && kt0 < qwl_abs - p.window + 1) ||
                                        kpartial);
@@ -409,7 +428,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
-              sacc[nb][r] = off <= hi ? sacc[nb][r] : kNegInf;
+              sacc[nb][r] = off <= hi ? sacc[nb][r] : kMasked;
             }
           }
         } else {
@@ -419,7 +438,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int off = 32 * nb + 8 * (r >> 2) + (r & 3);
-              sacc[nb][r] = (off >= lo && off <= hi) ? sacc[nb][r] : kNegInf;
+              sacc[nb][r] = (off >= lo && off <= hi) ? sacc[nb][r] : kMasked;
             }
           }
         }
@@ -437,7 +456,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
             const int key = key0 + off;
             const bool ok = key < Skv && (!p.causal || key <= qa) &&
                             (p.window <= 0 || key >= qa - p.window + 1) && ((kbits >> off) & 1u);
-            sacc[nb][r] = ok ? sacc[nb][r] : kNegInf;
+            sacc[nb][r] = ok ? sacc[nb][r] : kMasked;
           }
         }
       }
@@ -453,13 +472,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     // first and move m_run when it grows by more than kRescaleThresh.
     constexpr bool CHUNK_CHECK = IL;
     if constexpr (!CHUNK_CHECK) {
-      float mt = kNegInf;
-#pragma unroll
-      for (int nb = 0; nb < S::NB; ++nb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[nb][r]);
-      }
-      mt = wave_pair_max(mt);
+      const float mt = tile_max();
       const float m_new = fmaxf(m_run, mt);
       const bool need = m_new > m_run + kRescaleThresh / c;
       if (__any(need)) {
@@ -476,8 +489,14 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     }
     bool checked = !CHUNK_CHECK;  // uniform: this tile's max is known, later chunks are safe
     auto chunk_exp = [&](int nb, int base, float (&pv)[8]) __attribute__((always_inline)) {
+      if constexpr (SOFTCAP) {
+        const float cn = c + negmc;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(sacc[nb][base + e], c, negmc));
+        for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(sacc[nb][base + e], -2.0f * c, cn));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(sacc[nb][base + e], c, negmc));
+      }
       return ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
     };
 #pragma unroll
@@ -508,13 +527,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       float csum = chunk_exp(nb, base, pv);
       if (!checked && __any(!(csum <= lim))) {
         checked = true;
-        float mt = kNegInf;
-#pragma unroll
-        for (int nb2 = 0; nb2 < S::NB; ++nb2) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sacc[nb2][r]);
-        }
-        mt = wave_pair_max(mt);
+        const float mt = tile_max();
         const float m_new = fmaxf(m_run, mt);
         const float alpha = m_new > m_run ? fast_exp2((m_run - m_new) * c) : 1.0f;
         m_run = m_new;
