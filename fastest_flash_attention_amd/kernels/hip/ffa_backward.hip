@@ -998,6 +998,7 @@ void launch_f32_dp(const BwdParams& p, hipStream_t s) {
 // Rows are padded by 4 floats (the forward fp32 kernel's conflict-free pitch).
 // ---------------------------------------------------------------------------------
 constexpr int kM32 = 32;  // keys or rows per workgroup, rows per tile
+static_assert(F32WaveTile<64>::ROWS == kM32, "a wave tile is one 32-row tile");
 
 // dims [g DP/2, (g + 1) DP/2) of one fp32 row (zero past D): the stationary operand
 template <int DP>

@@ -891,6 +891,7 @@ __global__ __launch_bounds__(kThreads, kF32SplitBlocks<DP>) void prefill_f32_spl
   constexpr int HALF = DP / 2;
   constexpr int DB = DP / 32;
   constexpr int NE = 16 * DB + 2;  // floats per lane in the merge: O^T, m, l
+  static_assert(T::ROWS == kF32BN, "a wave tile is one key tile");
   static_assert(3 * NE * 64 <= 4 * 2 * kF32BN * PITCH, "merge fits in the tiles");
   __shared__ __attribute__((aligned(16))) float lds[4 * 2 * kF32BN * PITCH];
   const float* qf = reinterpret_cast<const float*>(p.q);
