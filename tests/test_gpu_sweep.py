@@ -1,0 +1,103 @@
+"""A seeded sweep of mixed shapes through the public API, forward and backward, against
+the oracle: head_dim 16-256 (padded widths included), bf16 / fp16 / fp32, GQA ratios,
+square and ragged lengths, kv_cache offsets (including more queries than keys, which
+leaves fully masked rows), causal / window / softcap in every combination. The cases
+are drawn once from a fixed seed, so every run checks the same list; they complement
+the hand-picked cases of the other files with combinations nobody chose."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import fastest_flash_attention_amd as ffa
+from oracle import reference_backward as rb
+from oracle import reference_forward as rf
+from tests.gpu_util import assert_parity, np32, require_gpu, say, seeded
+from tests.test_gpu_backward import _check, _oracle_forward
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+DIMS = (16, 24, 40, 64, 72, 96, 128, 136, 160, 192, 256)
+
+
+def _draw(n: int, seed: int, with_cache: bool):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice(DIMS))
+        dt = DTYPES[int(rng.integers(len(DTYPES)))]
+        Hkv = int(rng.choice((1, 2, 4)))
+        Hq = Hkv * int(rng.choice((1, 2, 4)))
+        B = int(rng.integers(1, 3))
+        Sq = int(rng.integers(1, 260))
+        Skv = Sq if rng.random() < 0.5 else int(rng.integers(1, 300))
+        cache = int(rng.integers(1, 200)) if with_cache and rng.random() < 0.35 else 0
+        causal = bool(rng.random() < 0.6)
+        window = int(rng.integers(1, 150)) if rng.random() < 0.35 else None
+        softcap = float(rng.choice((10.0, 30.0, 50.0))) if rng.random() < 0.3 else None
+        name = (f"{i}_B{B}_H{Hq}-{Hkv}_S{Sq}x{Skv}+{cache}_D{D}_{str(dt)[6:]}"
+                f"_c{int(causal)}_w{window}_cap{softcap}")
+        cases.append((name, B, Hq, Hkv, Sq, Skv, cache, D, dt, causal, window, softcap))
+    return cases
+
+
+FWD_CASES = _draw(48, 20261202, with_cache=True)
+BWD_CASES = _draw(32, 20261203, with_cache=False)
+
+
+@pytest.mark.parametrize("case", FWD_CASES, ids=[c[0] for c in FWD_CASES])
+def test_forward_sweep(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, cache, D, dt, causal, window, softcap = case
+    seed = 7 + 13 * int(name.split("_")[0])
+    q = seeded((B, Hq, Sq, D), dt, seed)
+    k = seeded((B, Hkv, Skv, D), dt, seed + 1)
+    v = seeded((B, Hkv, Skv, D), dt, seed + 2)
+    kw = dict(causal=causal, sliding_window=window, softcap=softcap, return_lse=True)
+    if Hq != Hkv:
+        kw["num_kv_heads"] = Hkv
+    kv_cache = None
+    if cache:
+        kv_cache = (seeded((B, Hkv, cache, D), dt, seed + 3), seeded((B, Hkv, cache, D), dt, seed + 4))
+    say(f"forward sweep {name}")
+    o, lse = ffa.fastest_flash_attn_forward(
+        q.cuda(), k.cuda(), v.cuda(),
+        kv_cache=None if kv_cache is None else (kv_cache[0].cuda(), kv_cache[1].cuda()), **kw)
+    torch.cuda.synchronize()
+    assert o.dtype == dt and o.shape == q.shape
+    ro, rl = rf.forward(np32(q), np32(k), np32(v),
+                        kv_cache=None if kv_cache is None else (np32(kv_cache[0]), np32(kv_cache[1])),
+                        **kw)
+    max_abs, _ = assert_parity(o, ro, lse, rl, name)
+    if dt == torch.float32:
+        assert max_abs < 1e-4, f"{name}: fp32 max-abs {max_abs:.2e}"
+
+
+@pytest.mark.parametrize("case", BWD_CASES, ids=[c[0] for c in BWD_CASES])
+def test_backward_sweep(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, _, D, dt, causal, window, softcap = case
+    seed = 11 + 17 * int(name.split("_")[0])
+    q = seeded((B, Hq, Sq, D), dt, seed)
+    k = seeded((B, Hkv, Skv, D), dt, seed + 1)
+    v = seeded((B, Hkv, Skv, D), dt, seed + 2)
+    do = seeded((B, Hq, Sq, D), dt, seed + 3)
+    scale = 1.0 / math.sqrt(D)
+    o32, lse = _oracle_forward(q, k, v, scale=scale, causal=causal, window=window,
+                               softcap=softcap, q_offset=0)
+    o = torch.from_numpy(o32).to(dt)
+    say(f"backward sweep {name}")
+    dq, dk, dv = ffa.fastest_flash_attn_backward(
+        do.cuda(), q.cuda(), k.cuda(), v.cuda(), o.cuda(), torch.from_numpy(lse).cuda(),
+        scale=scale, causal=causal, softcap=softcap, sliding_window=window)
+    torch.cuda.synchronize()
+    rq, rk, rv = rb.backward(np32(do), np32(q), np32(k), np32(v), np32(o), lse, scale=scale,
+                             causal=causal, softcap=softcap, sliding_window=window)
+    _check(dq, rq, dt, f"{name} dq")
+    _check(dk, rk, dt, f"{name} dk")
+    _check(dv, rv, dt, f"{name} dv")
