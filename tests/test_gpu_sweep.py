@@ -101,3 +101,49 @@ def test_backward_sweep(case):
     _check(dq, rq, dt, f"{name} dq")
     _check(dk, rk, dt, f"{name} dk")
     _check(dv, rv, dt, f"{name} dv")
+
+
+def _draw_decode(n: int, seed: int):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice((32, 64, 96, 128, 192, 256)))
+        dt = (torch.bfloat16, torch.float16)[int(rng.integers(2))]
+        Hkv = int(rng.choice((1, 2, 4, 8)))
+        Hq = Hkv * int(rng.choice((1, 2, 4, 8)))
+        P = int(rng.choice((4, 8, 12, 16, 32, 64)))
+        nseq = int(rng.integers(1, 6))
+        lens = [int(x) for x in rng.integers(0, 1500, size=nseq)]
+        window = int(rng.integers(1, 400)) if rng.random() < 0.3 else None
+        softcap = float(rng.choice((20.0, 50.0))) if rng.random() < 0.3 else None
+        tps = int(rng.choice((0, 32, 64, 256, 1024)))
+        name = (f"{i}_L{'-'.join(map(str, lens))}_H{Hq}-{Hkv}_D{D}_P{P}_{str(dt)[6:]}"
+                f"_w{window}_cap{softcap}_tps{tps}")
+        cases.append((name, lens, Hq, Hkv, D, P, dt, window, softcap, tps or None))
+    return cases
+
+
+DEC_CASES = _draw_decode(24, 20261204)
+
+
+@pytest.mark.parametrize("case", DEC_CASES, ids=[c[0] for c in DEC_CASES])
+def test_paged_decode_sweep(case):
+    require_gpu()
+    from oracle import paged as opaged
+    from tests.test_gpu_decode import _build_pool
+
+    name, lens, Hq, Hkv, D, P, dt, window, softcap, tps = case
+    idx = int(name.split("_")[0])
+    k_pages, v_pages, bt = _build_pool(lens, Hkv, D, P, dt, seed=100 + idx)
+    q = seeded((len(lens), Hq, D), dt, 200 + idx)
+    kw = dict(sliding_window=window, softcap=softcap)
+    say(f"decode sweep {name}")
+    o, lse = ffa.fastest_flash_paged_decode(q.cuda(), k_pages.cuda(), v_pages.cuda(), bt.cuda(),
+                                            torch.tensor(lens, dtype=torch.int32).cuda(),
+                                            return_lse=True, tokens_per_split=tps, **kw)
+    torch.cuda.synchronize()
+    ro, rl = opaged.paged_decode(np32(q), np32(k_pages), np32(v_pages), bt.numpy(), lens, **kw)
+    assert_parity(o, ro, lse, rl, name)
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert torch.all(o[b] == 0) and torch.all(torch.isneginf(lse[b]))
