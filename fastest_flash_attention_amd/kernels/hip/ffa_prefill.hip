@@ -556,8 +556,15 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   if (n_it > 0) {
     issue_k(tile_at(0), k_lds[0]);
     issue_v(tile_at(0), v_lds[0]);
-    if (n_it > 1) issue_k(tile_at(1), k_lds[1]);
-    wait_vmcnt0();
+    // S^T(0) needs K(0) only: the loads retire in issue order, so waiting until V(0)
+    // and K(1) alone may be outstanding leaves K(0) complete, and their latency
+    // overlaps S^T(0) (the first step's wait and barrier cover them)
+    if (n_it > 1) {
+      issue_k(tile_at(1), k_lds[1]);
+      wait_vmcnt<2 * S::LPT>();
+    } else {
+      wait_vmcnt<S::LPT>();
+    }
     __syncthreads();
     if (wave_live) qk(k_lds[0], s_cur);
   }
