@@ -48,15 +48,18 @@ constexpr void prefill_work_item(int bid, int grid, int n_qt, int xcd_group, int
 }
 
 // The prefill launcher's choice: causal grids (whose tiles differ in weight) with
-// n_units % 8 == 0 interleave the last two units of each XCD (on MI355X +2-3 % at
-// S = 8192 and +4-8 % at S = 4096 over unit after unit, for 1.26 GB of HBM reads per
-// north-star launch against 1.00; all units in interleaved pairs is as fast but reads
-// 1.51 GB, in fours 2.86 GB); other grids that split evenly over the XCDs keep
-// consecutive ids on one XCD.
+// n_units % 8 == 0 interleave the last units of each XCD: all of them when an XCD has at
+// most 8 (cfg3 and cfg5: 64 units), else the last four for units of at most 32 tiles
+// (cfg2) and the last two for longer ones (the north star). On MI355X, over unit after
+// unit: +2-3 % at S = 8192 and +4-8 % at S = 4096 for the last two; then all 8 +2 % at
+// cfg3 and +3.5 % at cfg5, the last four +1.5 % at cfg2 (-0.5 % at the north star,
+// all 16 there -2.6 %). Other grids that split evenly over the XCDs keep consecutive
+// ids on one XCD.
 constexpr void prefill_grid_order(bool causal, int64_t n_units, int64_t grid, int& xcd_group,
                                   int& xcd_remap) {
   xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  xcd_group = (causal && n_units % 8 == 0) ? 2 : 0;
+  const int64_t n_qt = n_units > 0 ? grid / n_units : 0;
+  xcd_group = (causal && n_units % 8 == 0) ? (n_units / 8 <= 8 ? 8 : (n_qt <= 32 ? 4 : 2)) : 0;
 }
 
 // Backward (dK/dV and dQ grids): grid = n_units * n_t, tile j = 0 the heaviest causal
