@@ -9,8 +9,8 @@ context lengths U[512, 32768], random page permutation), a third: MLA decode ove
 compressed latent cache (BASELINE cfg5 decode: batch 32 at context 4096), and a fourth:
 the attention backward at the north-star shape.
 
-Algorithmic work: prefill FLOPs = 4 * B * H * D * N_valid, N_valid = exact number of
-unmasked (q, k) pairs; decode bytes = K/V bytes of exactly context_len tokens + q + o +
+Algorithmic work: prefill FLOPs = 2 * B * H * (D + Dv) * N_valid (= 4 * B * H * D * N_valid
+where V has q's head dim), N_valid = exact number of unmasked (q, k) pairs; decode bytes = K/V bytes of exactly context_len tokens + q + o +
 lse + block tables + context lengths (split-K workspace traffic not counted).
 
 Timing: HIP events recorded on the stream the kernels launch on (torch's current
@@ -37,7 +37,10 @@ PREFILL = {
     "north_star": dict(B=4, Hq=32, Hkv=32, S=8192, D=128, causal=True, window=None, softcap=None),
     "cfg2": dict(B=4, Hq=32, Hkv=32, S=4096, D=128, causal=True, window=None, softcap=None),
     "cfg3": dict(B=2, Hq=32, Hkv=8, S=8192, D=128, causal=True, window=4096, softcap=50.0),
-    "cfg5": dict(B=2, Hq=32, Hkv=32, S=4096, D=192, causal=True, window=None, softcap=None),
+    # the MLA module's attention call: q / k of 128 + 64 rope dims, V at its 128 dims
+    # (taken as zero-padded to 192, as the reference pads it; no work on the pad)
+    "cfg5": dict(B=2, Hq=32, Hkv=32, S=4096, D=192, Dv=128, causal=True, window=None,
+                 softcap=None),
 }
 
 
@@ -137,10 +140,13 @@ def cpu_baseline_prefill(cfg: dict, q, k, v, budget_s: float) -> dict:
     """Oracle restatement of the reference CPU path (numpy, the reference dispatcher's
     block size) over whole (batch 0, head h) slices, h = 0, 1, ... until the time
     budget is spent; FLOPs counted exactly for the heads processed."""
+    import torch
+
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import reference_forward as rf
 
     S, D, ratio = cfg["S"], cfg["D"], cfg["Hq"] // cfg["Hkv"]
+    Dv = cfg.get("Dv", D)
     bs = rf.auto_select_block_size(S, S, D)
     pairs = n_valid_pairs_fast(S, cfg["causal"], cfg["window"])
     secs, heads = 0.0, 0
@@ -148,14 +154,15 @@ def cpu_baseline_prefill(cfg: dict, q, k, v, budget_s: float) -> dict:
         h = heads
         qh = q[0:1, h:h + 1].float().numpy()
         kh = k[0:1, h // ratio:h // ratio + 1].float().numpy()
-        vh = v[0:1, h // ratio:h // ratio + 1].float().numpy()
+        vh = v[0:1, h // ratio:h // ratio + 1].float()
+        vh = torch.nn.functional.pad(vh, (0, D - Dv)).numpy()  # the reference's padded V
         t = time.perf_counter()
         rf.flash_attn_cpu_forward(qh, kh, vh, scale=1 / math.sqrt(D), causal=cfg["causal"],
                                   block_q=bs, block_kv=bs, softcap=cfg["softcap"],
                                   sliding_window=cfg["window"])
         secs += time.perf_counter() - t
         heads += 1
-    flops = 4.0 * D * pairs * heads
+    flops = 2.0 * (D + Dv) * pairs * heads
     return {
         "value": flops / secs / 1e12,
         "unit": "TFLOP/s",
@@ -176,12 +183,13 @@ def bench_prefill(name: str, steps: int, warmup: int, cpu_budget: float):
 
     cfg = PREFILL[name]
     B, Hq, Hkv, S, D = cfg["B"], cfg["Hq"], cfg["Hkv"], cfg["S"], cfg["D"]
+    Dv = cfg.get("Dv", D)
     g = torch.Generator().manual_seed(0)
     # BASELINE recipe: fp32 randn on the host in the order q, k, v, cast to bf16 on the
     # host (identical bits on both sides), then moved to HBM.
     q = torch.randn(B, Hq, S, D, generator=g).to(torch.bfloat16)
     k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
-    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, Dv, generator=g).to(torch.bfloat16)
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     kw = dict(causal=cfg["causal"], sliding_window=cfg["window"], softcap=cfg["softcap"])
     if Hq != Hkv:
@@ -192,7 +200,7 @@ def bench_prefill(name: str, steps: int, warmup: int, cpu_budget: float):
 
     ms_event, ms_wall = time_steps(step, steps, warmup)
     pairs = n_valid_pairs_fast(S, cfg["causal"], cfg["window"])
-    flops = 4.0 * B * Hq * D * pairs
+    flops = 2.0 * B * Hq * (D + Dv) * pairs
     achieved = flops / (ms_event * 1e-3) / 1e12
     cpu = cpu_baseline_prefill(cfg, q, k, v, cpu_budget) if cpu_budget > 0 else None
     return {
@@ -209,7 +217,7 @@ def bench_prefill(name: str, steps: int, warmup: int, cpu_budget: float):
             "traffic": profiled_traffic(f"prefill_kernel_{name}.md"),
         },
         "config": {"workload": f"{name}_prefill", "batch": B, "heads_q": Hq, "heads_kv": Hkv,
-                   "seq_len": S, "head_dim": D, "causal": cfg["causal"],
+                   "seq_len": S, "head_dim": D, "v_head_dim": Dv, "causal": cfg["causal"],
                    "sliding_window": cfg["window"], "softcap": cfg["softcap"],
                    "n_valid_pairs_per_head": pairs},
         "cpu_baseline": cpu,

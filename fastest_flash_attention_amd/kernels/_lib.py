@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime before libffa.so)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libffa.so")
 
-FFA_ABI_VERSION = 5
+FFA_ABI_VERSION = 6
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
 FFA_DTYPE_FP32 = 2
@@ -63,6 +63,7 @@ class PrefillArgs(ctypes.Structure):
         ("block_key_mask", ctypes.c_void_p),
         ("block_key_mask_words", ctypes.c_int32),
         ("block_visited", ctypes.c_void_p),
+        ("v_head_dim", ctypes.c_int32),
     ]
 
 

@@ -104,6 +104,14 @@ int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
   if (a == nullptr) return FFA_ERR_INVALID_ARG;
   if (!valid_dtype(a->dtype) && a->dtype != FFA_DTYPE_FP32) return FFA_ERR_UNSUPPORTED_DTYPE;
   if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  // a narrower V (taken as zero-padded): the head_dim 192 kernels with 128-dim V tiles
+  if (a->v_head_dim != 0 && a->v_head_dim != a->head_dim) {
+    if (!valid_dtype(a->dtype) || a->head_dim <= 128 || a->head_dim > 192 || a->v_head_dim < 1 ||
+        a->v_head_dim > 128) {
+      return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+    }
+    if (a->v_head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
+  }
   if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->seqlen_q < 0 || a->seqlen_kv < 0) {
     return FFA_ERR_INVALID_ARG;
   }

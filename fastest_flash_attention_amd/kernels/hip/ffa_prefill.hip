@@ -47,7 +47,13 @@ constexpr int kBlockM = 128;
 // With a block mask, a workgroup first lists the KV tiles that hold any visible key for
 // its rows and visits only those; sweeps longer than this many tiles visit every tile.
 constexpr int kMaxLiveTiles = 2048;
+// Key tile of the narrow-V kernels (head_dim 192, V <= 128 dims): K 2 x 24 KiB + V 2 x
+// 16 KiB of LDS still fit two workgroups per CU (the block mask's tile list is dynamic
+// LDS). On MI355X at the MLA prefill shape (B 2, H 32, S 4096, causal): 0.332 ms against
+// 0.351 ms with 32-key tiles and 0.397 ms for the zero-padded V on the 192-dim kernel.
+constexpr int kNarrowBN = 64;
 constexpr int kTileFull = 0x8000;  // list entry flag: the block mask keeps the whole tile
+constexpr size_t kLiveLdsBytes = 4 * sizeof(int) + kMaxLiveTiles * sizeof(uint16_t);
 // Workgroup -> (batch x head, query tile j; j = 0 is the heaviest causal tile): the
 // XCD-aware order of ffa_grid.h, with the group / remap the launcher chose.
 __device__ inline void work_item(const PrefillParams& p, int bid, int& bh, int& jq) {
@@ -74,14 +80,21 @@ struct Shape {
 template <int DP, bool SOFTCAP>
 constexpr int kMinBlocks = (DP == 64 && !SOFTCAP) ? 3 : (DP <= 192 ? 2 : 1);
 
-template <typename Tag, int DP, int BN, bool SOFTCAP>
+// DV: the V tile / O accumulator width (<= DP). It is DP except for head_dim 192 over
+// a V of at most 128 dims (the MLA prefill's V, which its caller would otherwise
+// zero-pad to 192): P V then runs over the 128 real dims only.
+template <typename Tag, int DP, int DV, int BN, bool SOFTCAP>
 __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_kernel(const PrefillParams p) {
-  using S = Shape<DP, BN>;
+  using S = Shape<DP, BN>;   // Q, K tiles, S^T
+  using SV = Shape<DV, BN>;  // V tiles, O^T
   using E = Elem<Tag>;
   __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][S::TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][S::TILE];
-  __shared__ uint16_t live_lds[kMaxLiveTiles];  // block mask: the tiles to visit
-  __shared__ int live_cnt[4];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][SV::TILE];
+  // Block mask: the tiles to visit, in dynamic LDS that only launches with a block mask
+  // request (kLiveLdsBytes), so that the K/V buffers alone set the occupancy otherwise.
+  extern __shared__ __attribute__((aligned(16))) int live_dyn[];
+  int* const live_cnt = live_dyn;                                       // [4]
+  uint16_t* const live_lds = reinterpret_cast<uint16_t*>(live_dyn + 4);  // [kMaxLiveTiles]
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -182,15 +195,23 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   // fetched is (P % CPR) ^ swz(row), clamped below head_dim (padding dims multiply a
   // zero Q dim or feed O dims that are never stored).
   const int dchunks = D >> 3;
-  uint32_t k_off[S::LPT], v_off[S::LPT];
+  constexpr bool NARROW = DV < DP;  // V (and O's computed dims) narrower than Q / K
+  const int dvchunks = NARROW ? p.Dv >> 3 : dchunks;
+  uint32_t k_off[S::LPT], v_off[SV::LPT];
 #pragma unroll
   for (int j = 0; j < S::LPT; ++j) {
     const int pos = (4 * j + wave) * 64 + lane;
     const int row = pos / S::CPR;
     const int q = pos - row * S::CPR;
     const int kc = min(q ^ kswz<DP>(row), dchunks - 1);
-    const int vc = min(q ^ vswz<DP>(row), dchunks - 1);
     k_off[j] = static_cast<uint32_t>(row * p.k_ss * 2 + kc * 16);
+  }
+#pragma unroll
+  for (int j = 0; j < SV::LPT; ++j) {
+    const int pos = (4 * j + wave) * 64 + lane;
+    const int row = pos / SV::CPR;
+    const int q = pos - row * SV::CPR;
+    const int vc = min(q ^ vswz<DV>(row), dvchunks - 1);
     v_off[j] = static_cast<uint32_t>(row * p.v_ss * 2 + vc * 16);
   }
   // The loads are issued from inline asm (wave-uniform tile base + 32-bit lane offset):
@@ -201,19 +222,20 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   const int64_t k_tile_bytes = static_cast<int64_t>(BN) * p.k_ss * 2;
   const int64_t v_tile_bytes = static_cast<int64_t>(BN) * p.v_ss * 2;
   const int t_full = Skv / BN;  // tiles below this index hold BN keys
-  auto issue_tile = [&](const char*& tb, int64_t tile_bytes, int64_t stride,
-                        const uint32_t (&off)[S::LPT], uint16_t* dst, int t) __attribute__((always_inline)) {
+  auto issue_tile = [&](auto shp, const char*& tb, int64_t tile_bytes, int64_t stride,
+                        const auto& off, uint16_t* dst, int t) __attribute__((always_inline)) {
+    using SH = decltype(shp);
     if (t < t_full) {
 #pragma unroll
-      for (int j = 0; j < S::LPT; ++j) {
+      for (int j = 0; j < SH::LPT; ++j) {
         load_lds16_async(tb, off[j], lds_addr(dst + (4 * j + wave) * 512));
       }
     } else {
       // last tile: rows past Skv re-read row Skv-1 (their scores are masked to -inf)
       const int kt0 = t * BN;
 #pragma unroll
-      for (int j = 0; j < S::LPT; ++j) {
-        const int row = ((4 * j + wave) * 64 + lane) / S::CPR;
+      for (int j = 0; j < SH::LPT; ++j) {
+        const int row = ((4 * j + wave) * 64 + lane) / SH::CPR;
         const int over = max(0, kt0 + row - (Skv - 1));
         const uint32_t back = static_cast<uint32_t>(over * stride * 2);
         load_lds16_async(tb, off[j] - back, lds_addr(dst + (4 * j + wave) * 512));
@@ -226,12 +248,13 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   const uint32_t k_wlds = __builtin_amdgcn_readfirstlane(lds_addr(&k_lds[0][0]) + wave * 1024);
   const uint32_t v_wlds = __builtin_amdgcn_readfirstlane(lds_addr(&v_lds[0][0]) + wave * 1024);
   // A tile known to hold BN keys (no tail handling, no test) into buffer B.
-  auto issue_full = [&](const char*& tb, int64_t tile_bytes, const uint32_t (&off)[S::LPT],
+  auto issue_full = [&](auto shp, const char*& tb, int64_t tile_bytes, const auto& off,
                         uint32_t wlds, auto buf) __attribute__((always_inline)) {
+    using SH = decltype(shp);
     constexpr uint32_t B = decltype(buf)::value;
 #pragma unroll
-    for (int j = 0; j < S::LPT; ++j) {
-      load_lds16_async(tb, off[j], wlds + B * S::TILE * 2 + j * 4096);
+    for (int j = 0; j < SH::LPT; ++j) {
+      load_lds16_async(tb, off[j], wlds + B * SH::TILE * 2 + j * 4096);
     }
     tb += tile_bytes;
   };
@@ -241,31 +264,34 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   // list can jump, so there the pointer is set from t first.
   auto issue_k = [&](int t, uint16_t* dst) __attribute__((always_inline)) {
     if (use_list) k_next = kbytes + static_cast<int64_t>(t) * k_tile_bytes;
-    issue_tile(k_next, k_tile_bytes, p.k_ss, k_off, dst, t);
+    issue_tile(S{}, k_next, k_tile_bytes, p.k_ss, k_off, dst, t);
   };
   auto issue_v = [&](int t, uint16_t* dst) __attribute__((always_inline)) {
     if (use_list) v_next = vbytes + static_cast<int64_t>(t) * v_tile_bytes;
-    issue_tile(v_next, v_tile_bytes, p.v_ss, v_off, dst, t);
+    issue_tile(SV{}, v_next, v_tile_bytes, p.v_ss, v_off, dst, t);
   };
 
   // ---- per-lane LDS operand addresses (element offsets inside one tile buffer) ----
-  // K operand of k-step ks for 32-key block nb: row 32nb + l32, chunk 2ks + g.
-  int k_rd[S::KS];
+  // K operand of k-step ks for 32-key block nb: row 32nb + l32, chunk 2ks + g. The row
+  // swizzle XORs only the low log2(KSW) bits of the chunk index, so the address is a
+  // per-lane part for ks % KP plus the compile-time KSW * 8 * (ks / KP) (one register
+  // per KP k-steps instead of one per k-step: 4 rather than 12 at head_dim 192).
+  constexpr int KSW = (DP == 32) ? 4 : (DP == 64 || DP == 192) ? 8 : 16;
+  constexpr int KP = KSW / 2 < S::KS ? KSW / 2 : S::KS;
+  int k_rd4[KP];
 #pragma unroll
-  for (int ks = 0; ks < S::KS; ++ks) {
-    const int row = l32;
-    k_rd[ks] = row * DP + (((2 * ks + g) ^ kswz<DP>(row)) << 3);
-  }
+  for (int kp = 0; kp < KP; ++kp) k_rd4[kp] = l32 * DP + (((2 * kp + g) ^ kswz<DP>(l32)) << 3);
+  auto k_rd = [&](int ks) __attribute__((always_inline)) { return k_rd4[ks % KP] + KSW * 8 * (ks / KP); };
   // V^T operand of dim block db: this lane supplies row (key) rowoff of a 4-key group
   // and dims colw .. colw+3 of the block (ds_read_b64_tr_b16 law: lanes 4k..4k+3 of a
   // 16-lane group supply row k, lane i receives dim i of rows 0..3).
   const int rowoff = 4 * g + ((lane & 15) >> 2);
   const int colw = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  int v_rd[S::DB];
+  int v_rd[SV::DB];
 #pragma unroll
-  for (int db = 0; db < S::DB; ++db) {
+  for (int db = 0; db < SV::DB; ++db) {
     const int cg = 4 * db + (colw >> 3);
-    v_rd[db] = rowoff * DP + ((cg ^ vswz<DP>(rowoff)) << 3) + (colw & 7);
+    v_rd[db] = rowoff * DV + ((cg ^ vswz<DV>(rowoff)) << 3) + (colw & 7);
   }
 
   // Q^T as the B operand: lane holds row qrow (clamped: rows past Sq are never
@@ -284,9 +310,9 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     }
   }
 
-  f32x16 oacc[S::DB];
+  f32x16 oacc[SV::DB];
 #pragma unroll
-  for (int db = 0; db < S::DB; ++db) {
+  for (int db = 0; db < SV::DB; ++db) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
   }
@@ -305,18 +331,18 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     u32x4 a_cur[S::NB], a_nxt[S::NB];
 #pragma unroll
     for (int nb = 0; nb < S::NB; ++nb) {
-      a_cur[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd[0] + nb * 32 * DP);
+      a_cur[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd(0) + nb * 32 * DP);
     }
     // head_dim 192 (32-key tiles, one 32-key block): the 12 k-steps would form one chain
     // of dependent MFMAs, so even and odd k-steps go to two accumulators summed at the
     // end (+2.3 % at cfg5 on MI355X; with softcap it spills, and at 256 it is slower)
-    if constexpr (DP == 192 && !SOFTCAP) {
+    if constexpr (DP == 192 && BN == 32 && !SOFTCAP) {
       f32x16 s_odd;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s_odd[r] = 0.0f;
 #pragma unroll
       for (int ks = 0; ks < S::KS; ++ks) {
-        if (ks + 1 < S::KS) a_nxt[0] = *reinterpret_cast<const u32x4*>(kl + k_rd[ks + 1]);
+        if (ks + 1 < S::KS) a_nxt[0] = *reinterpret_cast<const u32x4*>(kl + k_rd(ks + 1));
         __builtin_amdgcn_sched_barrier(0);
         if (ks & 1) {
           s_odd = E::mfma32(a_cur[0], qreg[ks], s_odd);
@@ -334,7 +360,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       if (ks + 1 < S::KS) {
 #pragma unroll
         for (int nb = 0; nb < S::NB; ++nb) {
-          a_nxt[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd[ks + 1] + nb * 32 * DP);
+          a_nxt[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd(ks + 1) + nb * 32 * DP);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -369,7 +395,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       for (int ks = S::KS * cc / S::NC; ks < S::KS * (cc + 1) / S::NC; ++ks) {
 #pragma unroll
         for (int nb = 0; nb < S::NB; ++nb) {
-          ak[ks - S::KS * cc / S::NC][nb] = *reinterpret_cast<const u32x4*>(kl + k_rd[ks] + nb * 32 * DP);
+          ak[ks - S::KS * cc / S::NC][nb] = *reinterpret_cast<const u32x4*>(kl + k_rd(ks) + nb * 32 * DP);
         }
       }
     };
@@ -480,7 +506,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
         m_run = need ? m_new : m_run;
         l_run *= alpha;
 #pragma unroll
-        for (int db = 0; db < S::DB; ++db) {
+        for (int db = 0; db < SV::DB; ++db) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
         }
@@ -505,12 +531,12 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       const int base = (cc & 1) * 8;
       chunk_hook(cc);
       // V^T operands of the chunk first: their LDS latency overlaps the exp work
-      u32x4 av[S::DB];
+      u32x4 av[SV::DB];
 #pragma unroll
-      for (int db = 0; db < S::DB; ++db) {
-        const uint16_t* r0 = vl + v_rd[db] + 16 * cc * DP;
+      for (int db = 0; db < SV::DB; ++db) {
+        const uint16_t* r0 = vl + v_rd[db] + 16 * cc * DV;
         const u32x2 lo2 = lds_read_tr16(r0);             // keys 16cc + 4g + 0..3
-        const u32x2 hi2 = lds_read_tr16(r0 + 8 * DP);    // keys 16cc + 8 + 4g + 0..3
+        const u32x2 hi2 = lds_read_tr16(r0 + 8 * DV);    // keys 16cc + 8 + 4g + 0..3
         av[db] = u32x4{lo2[0], lo2[1], hi2[0], hi2[1]};
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -533,7 +559,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
         m_run = m_new;
         l_run *= alpha;
 #pragma unroll
-        for (int db = 0; db < S::DB; ++db) {
+        for (int db = 0; db < SV::DB; ++db) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
         }
@@ -546,7 +572,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       const u32x4 pk = {E::pack2(pv[0], pv[1]), E::pack2(pv[2], pv[3]),
                         E::pack2(pv[4], pv[5]), E::pack2(pv[6], pv[7])};
 #pragma unroll
-      for (int db = 0; db < S::DB; ++db) oacc[db] = E::mfma32(av[db], pk, oacc[db]);
+      for (int db = 0; db < SV::DB; ++db) oacc[db] = E::mfma32(av[db], pk, oacc[db]);
       if (IL && do_qk && cc + 1 < S::NC) rd_k(cc + 1);
     }
   };
@@ -557,13 +583,14 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     issue_k(tile_at(0), k_lds[0]);
     issue_v(tile_at(0), v_lds[0]);
     // S^T(0) needs K(0) only: the loads retire in issue order, so waiting until V(0)
-    // and K(1) alone may be outstanding leaves K(0) complete, and their latency
-    // overlaps S^T(0) (the first step's wait and barrier cover them)
+    // and K(1) alone may be outstanding (SV::LPT + S::LPT loads per thread; V tiles
+    // are narrower than K tiles in the narrow-V kernels) leaves K(0) complete, and
+    // their latency overlaps S^T(0) (the first step's wait and barrier cover them)
     if (n_it > 1) {
       issue_k(tile_at(1), k_lds[1]);
-      wait_vmcnt<2 * S::LPT>();
+      wait_vmcnt<SV::LPT + S::LPT>();
     } else {
-      wait_vmcnt<S::LPT>();
+      wait_vmcnt<SV::LPT>();
     }
     __syncthreads();
     if (wave_live) qk(k_lds[0], s_cur);
@@ -594,8 +621,8 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     wait_vmcnt0();
     __syncthreads();
     if (!IL) {
-      issue_full(k_next, k_tile_bytes, k_off, k_wlds, std::integral_constant<uint32_t, PAR>{});
-      issue_full(v_next, v_tile_bytes, v_off, v_wlds, std::integral_constant<uint32_t, 1 - PAR>{});
+      issue_full(S{}, k_next, k_tile_bytes, k_off, k_wlds, std::integral_constant<uint32_t, PAR>{});
+      issue_full(SV{}, v_next, v_tile_bytes, v_off, v_wlds, std::integral_constant<uint32_t, 1 - PAR>{});
       qk(k_lds[1 - PAR], nxt);
       softmax_pv(cur, t, v_lds[PAR], std::false_type{}, false, nxt, k_lds[1 - PAR], true, [](int) {});
     } else {
@@ -608,7 +635,10 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
 #pragma unroll
                    for (int j = S::LPT * cc / S::NC; j < S::LPT * (cc + 1) / S::NC; ++j) {
                      load_lds16_async(k_next, k_off[j], k_wlds + PAR * S::TILE * 2 + j * 4096);
-                     load_lds16_async(v_next, v_off[j], v_wlds + (1 - PAR) * S::TILE * 2 + j * 4096);
+                   }
+#pragma unroll
+                   for (int j = SV::LPT * cc / S::NC; j < SV::LPT * (cc + 1) / S::NC; ++j) {
+                     load_lds16_async(v_next, v_off[j], v_wlds + (1 - PAR) * SV::TILE * 2 + j * 4096);
                    }
                  });
       k_next += k_tile_bytes;
@@ -650,15 +680,20 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   if (wave_live && qrow < p.Sq) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;
+    const int Dv = NARROW ? p.Dv : D;
 #pragma unroll
-    for (int db = 0; db < S::DB; ++db) {
+    for (int db = 0; db < SV::DB; ++db) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d0 = 32 * db + 8 * i + 4 * g;
         const uint32_t w0 = E::pack2(oacc[db][4 * i + 0] * inv, oacc[db][4 * i + 1] * inv);
         const uint32_t w1 = E::pack2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
-        if (d0 < D) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{w0, w1};
+        if (d0 < Dv) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{w0, w1};
       }
+    }
+    // a V narrower than head_dim is zero-padded: O's dims past it are 0
+    if constexpr (NARROW) {
+      for (int d0 = Dv + 4 * g; d0 < D; d0 += 8) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{0u, 0u};
     }
     if (p.lse != nullptr && g == 0) {
       const float lse = l_tot > 0.0f ? (m_run * c + fast_log2(l_tot)) * kLn2
@@ -668,27 +703,32 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   }
 }
 
-template <typename Tag, int DP, int BN>
+template <typename Tag, int DP, int DV, int BN>
 void launch_dp(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
+  const size_t dyn = p.kmask != nullptr ? kLiveLdsBytes : 0;
   if (softcap) {
-    hipLaunchKernelGGL((prefill_kernel<Tag, DP, BN, true>), dim3(grid), dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((prefill_kernel<Tag, DP, DV, BN, true>), dim3(grid), dim3(kThreads), dyn, s, p);
   } else {
-    hipLaunchKernelGGL((prefill_kernel<Tag, DP, BN, false>), dim3(grid), dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((prefill_kernel<Tag, DP, DV, BN, false>), dim3(grid), dim3(kThreads), dyn, s, p);
   }
 }
 
 template <typename Tag>
 void launch_tag(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
   if (p.D <= 32) {
-    launch_dp<Tag, 32, 64>(p, softcap, grid, s);
+    launch_dp<Tag, 32, 32, 64>(p, softcap, grid, s);
   } else if (p.D <= 64) {
-    launch_dp<Tag, 64, 64>(p, softcap, grid, s);
+    launch_dp<Tag, 64, 64, 64>(p, softcap, grid, s);
   } else if (p.D <= 128) {
-    launch_dp<Tag, 128, 64>(p, softcap, grid, s);
+    launch_dp<Tag, 128, 128, 64>(p, softcap, grid, s);
   } else if (p.D <= 192) {
-    launch_dp<Tag, 192, 32>(p, softcap, grid, s);
+    if (p.Dv <= 128) {
+      launch_dp<Tag, 192, 128, kNarrowBN>(p, softcap, grid, s);
+    } else {
+      launch_dp<Tag, 192, 192, 32>(p, softcap, grid, s);
+    }
   } else {
-    launch_dp<Tag, 256, 32>(p, softcap, grid, s);
+    launch_dp<Tag, 256, 256, 32>(p, softcap, grid, s);
   }
 }
 
@@ -1168,6 +1208,7 @@ int launch_prefill(const ffa_prefill_args& a, hipStream_t stream) {
   p.Sq = a.seqlen_q;
   p.Skv = a.seqlen_kv;
   p.D = a.head_dim;
+  p.Dv = a.v_head_dim > 0 ? a.v_head_dim : a.head_dim;
   p.q_offset = a.q_offset;
   p.causal = a.causal ? 1 : 0;
   p.window = clamp_window(a.window, a.q_offset, a.seqlen_q);

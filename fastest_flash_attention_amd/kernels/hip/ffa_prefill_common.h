@@ -24,6 +24,7 @@ struct PrefillParams {
   int64_t o_sb, o_sh, o_ss;
   int64_t l_sb, l_sh, l_ss;
   int B, Hq, Hkv, Sq, Skv, D;
+  int Dv;  // V's head dim (<= D): O's dims past it are written as 0
   int q_offset, causal, window;
   int ratio;
   int n_qt;

@@ -88,9 +88,10 @@ class FastestFlashMLA(nn.Module):
         self.rope = RotaryEmbedding(rope_dim)
         self.o_proj = nn.Linear(num_heads * (head_dim + rope_dim), hidden_size, bias=False)
 
-    def project_qkv(self, x: torch.Tensor):
+    def project_qkv(self, x: torch.Tensor, pad_v: bool = True):
         """q, k, v_padded ``[B, H, S, head_dim + rope_dim]`` as the reference builds
-        them (:129-152)."""
+        them (:129-152); with ``pad_v=False`` V stays ``[B, H, S, head_dim]`` (a view of
+        the up-projection's output)."""
         B, S, _ = x.shape
         H = self.num_heads
         q_nope = self.q_proj(x).view(B, S, H, self.head_dim).transpose(1, 2)
@@ -102,6 +103,8 @@ class FastestFlashMLA(nn.Module):
         k_rope = self.k_rope_proj(x).unsqueeze(1).expand(-1, H, -1, -1)
         k_rope = self.rope(k_rope)
         k = torch.cat([k_nope, k_rope], dim=-1)
+        if not pad_v:
+            return q, k, v
         v_padded = torch.nn.functional.pad(v, (0, self.rope_dim))
         return q, k, v_padded
 
@@ -111,12 +114,16 @@ class FastestFlashMLA(nn.Module):
         B, S, _ = x.shape
         use_causal = self.default_causal if causal is None else causal
         bs = block_size or self.block_size or None
-        q, k, v_padded = self.project_qkv(x)
         if self.training:
+            q, k, v_padded = self.project_qkv(x)
             attn = fastest_flash_attn_func(q, k, v_padded, scale=self.scale, causal=use_causal,
                                            block_size=bs or 64)
         else:
-            attn, _ = fastest_flash_attn_forward(q, k, v_padded, scale=self.scale,
+            # V at its own head_dim: the forward takes a narrower V as zero-padded (the
+            # same O as with v_padded, its rope_dim tail 0) and runs P V over the real
+            # dims only
+            q, k, v = self.project_qkv(x, pad_v=False)
+            attn, _ = fastest_flash_attn_forward(q, k, v, scale=self.scale,
                                                  causal=use_causal, block_size=bs)
         return self.o_proj(attn.transpose(1, 2).contiguous().view(B, S, -1))
 

@@ -53,6 +53,7 @@ class ResolvedForward:
     block_kv: int
     return_lse: bool
     squeezed: bool
+    Dv: int = 0  # v's head dim (<= D; a narrower v is taken as zero-padded to D)
 
 
 @dataclass
@@ -180,7 +181,10 @@ def resolve_forward_args(
         q_offset = k.size(2) - S_q
     S_kv = k.size(2)
 
-    if v.shape[:3] != k.shape[:3] or k.size(3) != D or v.size(3) != D:
+    # v may be narrower than q / k: it is then taken as zero-padded to D (the MLA
+    # module's V, which the reference pads itself, modules/flash_mla.py:151-152), and
+    # the output keeps q's shape
+    if v.shape[:3] != k.shape[:3] or k.size(3) != D or not 1 <= v.size(3) <= D:
         raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
     if H_q != H_kv:
         if num_kv_heads is None and H_kv != 1:
@@ -209,7 +213,7 @@ def resolve_forward_args(
         sliding_window=None if sliding_window is None else int(sliding_window),
         softcap=None if softcap is None else float(softcap), two_pass=bool(two_pass),
         compute_dtype=compute_dtype, block_mask=block_mask, block_q=int(bq),
-        block_kv=int(bkv), return_lse=bool(return_lse), squeezed=squeezed,
+        block_kv=int(bkv), return_lse=bool(return_lse), squeezed=squeezed, Dv=int(v.size(3)),
     )
 
 
@@ -244,6 +248,7 @@ def build_prefill_args(
     a.ref_block_kv = r.block_kv
     a.masked_lse_mode = 1 if r.two_pass else 0
     a.dtype = dtype_code
+    a.v_head_dim = r.Dv if 0 < r.Dv < r.D else 0
     return a
 
 
@@ -277,11 +282,17 @@ def prepare_prefill(*args, out: Optional[torch.Tensor] = None, **kwargs) -> Pref
     if r.D > 256:
         raise ValueError(f"head_dim {r.D} > 256 is not supported")
     d_pad = (r.D + 7) // 8 * 8
+    # A narrower v runs natively where the library has kernels for it (16-bit inputs,
+    # head_dim 129..192, v_head_dim <= 128 and a multiple of 8); elsewhere it is
+    # zero-padded here, which gives the same result.
+    narrow_v = (r.Dv < d_pad and code != _lib.FFA_DTYPE_FP32 and 128 < d_pad <= 192
+                and r.Dv <= 128 and r.Dv % 8 == 0)
     r.q = _conform(r.q, d_pad)
     r.k = _conform(r.k, d_pad)
-    r.v = _conform(r.v, d_pad)
+    r.v = _conform(r.v, r.Dv if narrow_v else d_pad)
     d_user = r.D
     r.D = d_pad
+    r.Dv = r.Dv if narrow_v else d_pad
     if out is None or d_pad != d_user:
         out = torch.empty((r.B, r.H_q, r.S_q, d_pad), dtype=r.q.dtype, device=r.q.device)
     lse = (

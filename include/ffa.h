@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FFA_ABI_VERSION 5
+#define FFA_ABI_VERSION 6
 
 typedef enum ffa_status {
   FFA_OK = 0,
@@ -137,6 +137,13 @@ typedef struct ffa_prefill_args {
   int32_t block_key_mask_words;    /* words per row block, >= ceil(seqlen_kv / 64) */
   const int32_t* block_visited;    /* [n_br] reference tiles visited per row block
                                       (required with block_key_mask) */
+  int32_t v_head_dim;  /* 0 or head_dim: v has head_dim dims. Otherwise v (and its
+                          strides) has v_head_dim < head_dim dims and is taken as
+                          zero-padded to head_dim: O dims >= v_head_dim are written 0,
+                          the result the reference gives for the zero-padded V that the
+                          MLA module builds (modules/flash_mla.py:151-152). Supported for
+                          bf16 / fp16 at head_dim 129..192 with v_head_dim <= 128, a
+                          multiple of 8 (FFA_ERR_UNSUPPORTED_HEAD_DIM otherwise). */
 } ffa_prefill_args;
 
 int ffa_prefill_fwd(const ffa_prefill_args* args, void* stream);

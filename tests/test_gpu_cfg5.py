@@ -52,14 +52,24 @@ def test_cfg5_prefill_full_size():
     x = _randn((B, S, HIDDEN), 1)
     say("cfg5 prefill B2 S4096 hidden 4096 H32 D192")
     with torch.no_grad():
-        q, k, vp = m.project_qkv(x)
-        assert q.shape == (B, HEADS, S, HEAD_DIM + ROPE)
-        attn, lse = ffa.fastest_flash_attn_forward(q, k, vp, scale=m.scale, causal=True,
+        # the module's own call: V at its 128 dims, taken as zero-padded to 192
+        q, k, v = m.project_qkv(x, pad_v=False)
+        assert q.shape == (B, HEADS, S, HEAD_DIM + ROPE) and v.shape[-1] == HEAD_DIM
+        attn, lse = ffa.fastest_flash_attn_forward(q, k, v, scale=m.scale, causal=True,
                                                    return_lse=True)
         out = m(x)
         torch.cuda.synchronize()
         assert torch.isfinite(attn).all() and torch.isfinite(lse).all()
         assert torch.equal(out, m.o_proj(attn.transpose(1, 2).reshape(B, S, -1)))
+        assert torch.all(attn[..., HEAD_DIM:] == 0)
+        # the reference's zero-padded V through the 192-dim kernel: the same O up to
+        # rounding (other key tiles), the same LSE
+        vp = torch.nn.functional.pad(v, (0, ROPE))
+        attn_p, lse_p = ffa.fastest_flash_attn_forward(q, k, vp, scale=m.scale, causal=True,
+                                                       return_lse=True)
+        d = (attn.float() - attn_p.float()).abs()
+        assert d.max().item() < 2e-2 and d.mean().item() < 2e-3, d.max().item()
+        assert (lse - lse_p).abs().max().item() < 1e-3
     # sampled (batch, head) pairs over both batches and the head range
     for b, h in ((0, 0), (0, 13), (1, 7), (1, 31)):
         for r0 in (0, 2048 - 64, S - 128):

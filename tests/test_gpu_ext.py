@@ -58,6 +58,28 @@ def test_block_mask_parity(case):
         assert np.all(np32(o)[:, :, :bs] == 0)
 
 
+def test_block_mask_narrow_v():
+    """A block mask on the narrow-V kernel (head_dim 192 over a 128-dim V taken as
+    zero-padded): its live-tile list sits in dynamic LDS beside the K/V buffers."""
+    require_gpu()
+    B, H, S, D, Dv, bs = 1, 4, 230, 192, 128, 32
+    q = seeded((B, H, S, D), BF16, 31)
+    k = seeded((B, H, S, D), BF16, 32)
+    v = seeded((B, H, S, Dv), BF16, 33)
+    g = torch.Generator().manual_seed(34)
+    bm = torch.rand(math.ceil(S / bs), math.ceil(S / bs), generator=g) < 0.6
+    bm[0, :] = False
+    say(f"block_mask narrow v B{B} H{H} S{S} D{D} Dv{Dv} bs{bs}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), block_size=bs,
+                                            block_mask=bm, causal=True, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.all(o[..., Dv:] == 0)
+    vp = torch.nn.functional.pad(v, (0, D - Dv))
+    ro, rl = rf.forward(np32(q), np32(k), np32(vp), block_size=bs, block_mask=bm.numpy(),
+                        causal=True, return_lse=True)
+    assert_parity(o, ro, lse, rl, "block_mask narrow v")
+
+
 # Masks that leave whole 64-key tiles of a workgroup's rows empty, so the kernel's
 # live-tile list skips them: (name, Sq, Skv, D, block, mask kind, kwargs)
 SKIP_CASES = [

@@ -60,11 +60,17 @@ def test_mla_module_d192():
     x = torch.randn(1, 130, 512, device="cuda").to(torch.bfloat16)
     say("module MLA")
     out = m(x)
-    q, k, vp = m.project_qkv(x)
-    assert q.shape[-1] == 192 and q.dtype == torch.bfloat16
-    a, _ = ffa.fastest_flash_attn_forward(q, k, vp, scale=m.scale, causal=True)
+    # eval mode passes V at its 128 dims (taken as zero-padded to 192)
+    q, k, v = m.project_qkv(x, pad_v=False)
+    assert q.shape[-1] == 192 and v.shape[-1] == 128 and q.dtype == torch.bfloat16
+    a, _ = ffa.fastest_flash_attn_forward(q, k, v, scale=m.scale, causal=True)
     assert torch.equal(out, m.o_proj(a.transpose(1, 2).reshape(1, 130, -1)))
     assert torch.isfinite(out).all()
+    # the same as the reference's zero-padded V, up to rounding
+    _, _, vp = m.project_qkv(x)
+    ap, _ = ffa.fastest_flash_attn_forward(q, k, vp, scale=m.scale, causal=True)
+    d = (a.float() - ap.float()).abs()
+    assert torch.all(a[..., 128:] == 0) and d.max().item() < 2e-2 and d.mean().item() < 2e-3
 
 
 def _mha_reference_fp32(m, x):

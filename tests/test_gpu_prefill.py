@@ -61,6 +61,40 @@ def test_prefill_parity(case):
     assert_parity(o, ro, lse, rl, name)
 
 
+# (name, B, Hq, Hkv, Sq, Skv, D, Dv, kwargs, dtype): v narrower than q / k, which the
+# forward takes as zero-padded to D (the MLA module passes its 128-dim V this way).
+# head_dim 129..192 with Dv <= 128 (a multiple of 8) runs the narrow-V kernels; the
+# last two shapes are zero-padded on the host.
+NARROW_V = [
+    ("mla_causal", 1, 4, 4, 300, 300, 192, 128, {"causal": True}, BF16),
+    ("mla_gqa_window_softcap", 2, 8, 2, 333, 333, 192, 128,
+     {"causal": True, "sliding_window": 100, "softcap": 50.0, "num_kv_heads": 2}, BF16),
+    ("mla_noncausal_ragged", 1, 2, 2, 77, 203, 192, 128, {}, BF16),
+    ("d136_dv64_fp16", 1, 2, 2, 100, 100, 136, 64, {"causal": True}, F16),
+    ("d160_dv120_window", 1, 2, 2, 260, 260, 160, 120, {"sliding_window": 50}, BF16),
+    ("mla_negative_scale", 1, 2, 2, 140, 140, 192, 128, {"causal": True, "scale": -0.1}, BF16),
+    ("host_padded_d128_dv64", 1, 2, 2, 90, 90, 128, 64, {"causal": True}, BF16),
+    ("host_padded_dv100", 1, 2, 2, 90, 90, 192, 100, {"causal": True}, BF16),
+]
+
+
+@pytest.mark.parametrize("case", NARROW_V, ids=[c[0] for c in NARROW_V])
+def test_prefill_narrow_v(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, D, Dv, kw, dt = case
+    q = seeded((B, Hq, Sq, D), dt, 11)
+    k = seeded((B, Hkv, Skv, D), dt, 12)
+    v = seeded((B, Hkv, Skv, Dv), dt, 13)
+    say(f"prefill narrow v {name} B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} Dv{Dv} {kw} {dt}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), return_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert o.shape == q.shape and o.dtype == dt
+    assert torch.all(o[..., Dv:] == 0), "O dims past v's must be 0"
+    vp = torch.nn.functional.pad(v, (0, D - Dv))
+    ro, rl = rf.forward(np32(q), np32(k), np32(vp), return_lse=True, **kw)
+    assert_parity(o, ro, lse, rl, name)
+
+
 def test_kv_cache_offset():
     require_gpu()
     B, H, D = 2, 4, 128

@@ -431,3 +431,34 @@ def test_abi_rejects_positions_beyond_int32_range(lib, field, value):
     a = _valid_prefill_args(0.125)
     setattr(a, field, value)
     assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == -9
+
+
+@pytest.mark.parametrize("head_dim,v_head_dim,dtype,code", [
+    (192, 128, _lib.FFA_DTYPE_FP32, -3),   # narrow V: 16-bit inputs only
+    (128, 64, _lib.FFA_DTYPE_BF16, -3),    # only head_dim 129..192
+    (256, 128, _lib.FFA_DTYPE_BF16, -3),
+    (192, 136, _lib.FFA_DTYPE_BF16, -3),   # v_head_dim <= 128
+    (192, 100, _lib.FFA_DTYPE_BF16, -4),   # a multiple of 8
+])
+def test_abi_narrow_v_contract(lib, head_dim, v_head_dim, dtype, code):
+    """A V narrower than head_dim (taken as zero-padded) is accepted only where the
+    library has kernels for it; everything else is rejected before any HIP call."""
+    a = _valid_prefill_args(0.125)
+    a.head_dim, a.v_head_dim, a.dtype = head_dim, v_head_dim, dtype
+    assert lib.ffa_prefill_fwd(ctypes.byref(a), None) == code
+
+
+def test_host_layer_narrow_v():
+    """The op keeps a narrower V unpadded where the kernels take it (16-bit, head_dim
+    129..192, v dims <= 128 and a multiple of 8) and zero-pads it elsewhere."""
+    q = torch.zeros(1, 2, 8, 192, dtype=torch.bfloat16)
+    v = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16)
+    r = af.resolve_forward_args(q, q, v)
+    assert (r.D, r.Dv) == (192, 128)
+    out = torch.empty_like(q)
+    a = af.build_prefill_args(r, out, None, _lib.FFA_DTYPE_BF16)
+    assert a.v_head_dim == 128 and a.head_dim == 192
+    r = af.resolve_forward_args(q, q, q)
+    assert af.build_prefill_args(r, out, None, _lib.FFA_DTYPE_BF16).v_head_dim == 0
+    with pytest.raises(ValueError):
+        af.resolve_forward_args(q[..., :64], q[..., :64], v)  # v wider than q

@@ -22,8 +22,9 @@ from fastest_flash_attention_amd.kernels.hip import build
 
 # kernel-name regex -> largest scratch bytes per lane allowed
 EXCEPTIONS = {
-    # head_dim 192 with softcap: the tanh work of 32-key tiles at 256 VGPRs
-    r"prefill_kernel<.*, 192, 32, true>": 16,
+    # narrow-V head_dim 192 with softcap: 64-key tiles at 256 VGPRs (still faster than
+    # 32-key tiles without spills, 0.391 vs 0.401 ms at the MLA prefill shape)
+    r"prefill_kernel<.*, 192, 128, 64, true>": 16,
 }
 
 
@@ -71,5 +72,5 @@ def test_hot_kernels_do_not_spill(tmp_path):
             bad.append(f"{name}: {priv} B scratch per lane (allowed {limit})")
     assert not bad, "\n".join(bad)
     # the headline kernel in particular
-    ns = [n for m, n in names.items() if re.search(r"prefill_kernel<ffa::Bf16Tag, 128, 64, false>", n)]
+    ns = [n for m, n in names.items() if re.search(r"prefill_kernel<ffa::Bf16Tag, 128, 128, 64, false>", n)]
     assert ns and all(scratch[m] == 0 for m, n in names.items() if n in ns)
