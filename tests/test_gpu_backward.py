@@ -198,6 +198,30 @@ def test_autograd_func_gqa_matches_oracle():
     _check(v.grad, rv, BF16, "gqa dv")
 
 
+def test_autograd_func_narrow_v():
+    """fastest_flash_attn_func with V narrower than q / k (the MLA shape: 192 / 128) is
+    the zero-padded-V call: the same output and dQ / dK bit for bit, and dV is the padded
+    call's dV on V's own dims."""
+    require_gpu()
+    B, H, S, D, Dv = 1, 4, 200, 192, 128
+    q = seeded((B, H, S, D), BF16, 41).cuda()
+    k = seeded((B, H, S, D), BF16, 42).cuda()
+    v = seeded((B, H, S, Dv), BF16, 43).cuda()
+    do = seeded((B, H, S, D), BF16, 44).cuda()
+    say("autograd func narrow v")
+    grads = []
+    for vv in (v, torch.nn.functional.pad(v, (0, D - Dv))):
+        qa, ka, va = (t.clone().requires_grad_() for t in (q, k, vv))
+        out = ffa.fastest_flash_attn_func(qa, ka, va, causal=True)
+        out.backward(do)
+        grads.append((out.detach(), qa.grad, ka.grad, va.grad))
+    torch.cuda.synchronize()
+    (o1, dq1, dk1, dv1), (o2, dq2, dk2, dv2) = grads
+    assert dv1.shape == v.shape
+    assert torch.equal(o1, o2) and torch.equal(dq1, dq2) and torch.equal(dk1, dk2)
+    assert torch.equal(dv1, dv2[..., :Dv])
+
+
 def test_autograd_func_fp32_matches_oracle():
     """Training in fp32 (the reference's default dtype): fp32 forward + fp32 backward
     through fastest_flash_attn_func, GQA with a window, against the oracle fed the HIP

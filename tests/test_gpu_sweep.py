@@ -147,3 +147,62 @@ def test_paged_decode_sweep(case):
     for b, L in enumerate(lens):
         if L == 0:
             assert torch.all(o[b] == 0) and torch.all(torch.isneginf(lse[b]))
+
+
+def _draw_narrow(n: int, seed: int):
+    """V narrower than q / k (taken as zero-padded to D): the narrow-V kernels for
+    16-bit inputs at head_dim 129..192 with V dims <= 128 and a multiple of 8, the
+    host zero-pad elsewhere (fp32, other widths)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice((136, 144, 160, 176, 192)))
+        Dv = int(rng.choice((8, 32, 64, 96, 120, 128, 100, 129))) if D > 129 else 64
+        Dv = min(Dv, D - 8)
+        dt = DTYPES[int(rng.choice((0, 0, 1, 2)))]
+        Hkv = int(rng.choice((1, 2, 4)))
+        Hq = Hkv * int(rng.choice((1, 2, 4)))
+        B = int(rng.integers(1, 3))
+        Sq = int(rng.integers(1, 260))
+        Skv = Sq if rng.random() < 0.5 else int(rng.integers(1, 300))
+        cache = int(rng.integers(1, 200)) if rng.random() < 0.3 else 0
+        causal = bool(rng.random() < 0.6)
+        window = int(rng.integers(1, 150)) if rng.random() < 0.35 else None
+        softcap = float(rng.choice((10.0, 30.0, 50.0))) if rng.random() < 0.3 else None
+        name = (f"{i}_B{B}_H{Hq}-{Hkv}_S{Sq}x{Skv}+{cache}_D{D}v{Dv}_{str(dt)[6:]}"
+                f"_c{int(causal)}_w{window}_cap{softcap}")
+        cases.append((name, B, Hq, Hkv, Sq, Skv, cache, D, Dv, dt, causal, window, softcap))
+    return cases
+
+
+NARROW_CASES = _draw_narrow(20, 20261204)
+
+
+@pytest.mark.parametrize("case", NARROW_CASES, ids=[c[0] for c in NARROW_CASES])
+def test_forward_sweep_narrow_v(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, cache, D, Dv, dt, causal, window, softcap = case
+    seed = 5 + 19 * int(name.split("_")[0])
+    q = seeded((B, Hq, Sq, D), dt, seed)
+    k = seeded((B, Hkv, Skv, D), dt, seed + 1)
+    v = seeded((B, Hkv, Skv, Dv), dt, seed + 2)
+    kw = dict(causal=causal, sliding_window=window, softcap=softcap, return_lse=True)
+    if Hq != Hkv:
+        kw["num_kv_heads"] = Hkv
+    kv_cache = None
+    if cache:
+        kv_cache = (seeded((B, Hkv, cache, D), dt, seed + 3), seeded((B, Hkv, cache, Dv), dt, seed + 4))
+    say(f"forward sweep narrow v {name}")
+    o, lse = ffa.fastest_flash_attn_forward(
+        q.cuda(), k.cuda(), v.cuda(),
+        kv_cache=None if kv_cache is None else (kv_cache[0].cuda(), kv_cache[1].cuda()), **kw)
+    torch.cuda.synchronize()
+    assert o.dtype == dt and o.shape == q.shape
+    assert torch.all(o[..., Dv:] == 0), f"{name}: O dims past v's must be 0"
+    pad = lambda t: np.pad(np32(t), [(0, 0)] * 3 + [(0, D - Dv)])
+    ro, rl = rf.forward(np32(q), np32(k), pad(v),
+                        kv_cache=None if kv_cache is None else (np32(kv_cache[0]), pad(kv_cache[1])),
+                        **kw)
+    max_abs, _ = assert_parity(o, ro, lse, rl, name)
+    if dt == torch.float32:
+        assert max_abs < 1e-4, f"{name}: fp32 max-abs {max_abs:.2e}"
