@@ -20,7 +20,7 @@ import torch  # noqa: F401  (must load torch's HIP runtime before libffa.so)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libffa.so")
 
-FFA_ABI_VERSION = 6
+FFA_ABI_VERSION = 7
 FFA_DTYPE_BF16 = 0
 FFA_DTYPE_FP16 = 1
 FFA_DTYPE_FP32 = 2
@@ -203,6 +203,7 @@ class AttnBwdArgs(ctypes.Structure):
         ("scale", ctypes.c_float),
         ("softcap", ctypes.c_float),
         ("dtype", ctypes.c_int32),
+        ("v_head_dim", ctypes.c_int32),
     ]
 
 

@@ -16,6 +16,16 @@ namespace {
 
 bool valid_dtype(int32_t dt) { return dt == FFA_DTYPE_BF16 || dt == FFA_DTYPE_FP16; }
 
+// A V narrower than head_dim (taken as zero-padded): the head_dim 192 kernels with
+// 128-dim V tiles. FFA_OK, or why the combination is rejected.
+int check_v_head_dim(int32_t v_head_dim, int32_t head_dim, int32_t dtype) {
+  if (v_head_dim == 0 || v_head_dim == head_dim) return FFA_OK;
+  if (!valid_dtype(dtype) || head_dim <= 128 || head_dim > 192 || v_head_dim < 1 || v_head_dim > 128) {
+    return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  }
+  return v_head_dim % 8 != 0 ? FFA_ERR_MISALIGNED : FFA_OK;
+}
+
 // scale: any finite value. softcap: <= 0 (none) or a finite positive cap.
 bool valid_scale(float scale, float softcap) {
   return std::isfinite(scale) && !std::isnan(softcap) && !(softcap > 0.0f && std::isinf(softcap));
@@ -104,14 +114,7 @@ int ffa_prefill_fwd(const ffa_prefill_args* a, void* stream) {
   if (a == nullptr) return FFA_ERR_INVALID_ARG;
   if (!valid_dtype(a->dtype) && a->dtype != FFA_DTYPE_FP32) return FFA_ERR_UNSUPPORTED_DTYPE;
   if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
-  // a narrower V (taken as zero-padded): the head_dim 192 kernels with 128-dim V tiles
-  if (a->v_head_dim != 0 && a->v_head_dim != a->head_dim) {
-    if (!valid_dtype(a->dtype) || a->head_dim <= 128 || a->head_dim > 192 || a->v_head_dim < 1 ||
-        a->v_head_dim > 128) {
-      return FFA_ERR_UNSUPPORTED_HEAD_DIM;
-    }
-    if (a->v_head_dim % 8 != 0) return FFA_ERR_MISALIGNED;
-  }
+  if (const int rc = check_v_head_dim(a->v_head_dim, a->head_dim, a->dtype); rc != FFA_OK) return rc;
   if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->seqlen_q < 0 || a->seqlen_kv < 0) {
     return FFA_ERR_INVALID_ARG;
   }
@@ -278,6 +281,7 @@ int ffa_attn_bwd(const ffa_attn_bwd_args* a, void* stream) {
   if (a == nullptr) return FFA_ERR_INVALID_ARG;
   if (!valid_dtype(a->dtype) && a->dtype != FFA_DTYPE_FP32) return FFA_ERR_UNSUPPORTED_DTYPE;
   if (a->head_dim < 1 || a->head_dim > 256) return FFA_ERR_UNSUPPORTED_HEAD_DIM;
+  if (const int rc = check_v_head_dim(a->v_head_dim, a->head_dim, a->dtype); rc != FFA_OK) return rc;
   if (a->batch < 0 || a->heads_q < 1 || a->heads_kv < 1 || a->seqlen_q < 0 || a->seqlen_kv < 0) {
     return FFA_ERR_INVALID_ARG;
   }

@@ -85,6 +85,7 @@ struct BwdParams {
   float scale;
   int xcd_remap_dq, xcd_remap_dkv;
   int xcd_group_dq, xcd_group_dkv;  // > 0: units per interleaved group on one XCD
+  int Dv;  // V's (and dV's) head dim, <= D: V is taken as zero-padded to D
 };
 
 // Workgroup -> (unit u = batch x head, tile j; j = 0 the heaviest causal tile): the
@@ -282,17 +283,25 @@ __global__ __launch_bounds__(kThreads) void bwd_pre_kernel(const BwdParams p) {
 template <int DP>
 constexpr int kBwdMinBlocks = DP <= 128 ? 2 : 1;
 
-template <typename Tag, int DP, bool SOFTCAP>
+// DV: the width of V, dO's used dims and dV (<= DP). It is DP except for head_dim 192
+// over a V of at most 128 dims (the MLA module's V, which the reference zero-pads):
+// with V's padding zero, dP = dO V^T needs dO's first DV dims only, and dV's padding
+// dims are not outputs, so dP and dV run over DV dims.
+template <typename Tag, int DP, int DV, bool SOFTCAP>
 __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(const BwdParams p) {
-  using S = BShape<DP>;
+  using S = BShape<DP>;   // Q, K, dK
+  using SV = BShape<DV>;  // dO, V, dV
   using E = Elem<Tag>;
   constexpr int TILE = kDkvRows * DP;
-  constexpr int LPT = kDkvRows * S::CPR / kThreads;  // tile loads per thread per tensor
-  static_assert(kDkvRows * S::CPR % kThreads == 0, "tile must split evenly");
+  constexpr int TILE_V = kDkvRows * DV;
+  constexpr int LPT = kDkvRows * S::CPR / kThreads;    // Q tile loads per thread
+  constexpr int LPTV = kDkvRows * SV::CPR / kThreads;  // dO tile loads per thread
+  static_assert(kDkvRows * S::CPR % kThreads == 0 && kDkvRows * SV::CPR % kThreads == 0,
+                "tile must split evenly");
   __shared__ __attribute__((aligned(1024))) uint16_t q_lds[2][TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t do_lds[2][TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t do_lds[2][TILE_V];
   __shared__ __attribute__((aligned(1024))) float st_lds[2][256];  // [0,32) lse2, [32,64) D_i
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[4][32 * DP];  // each wave's V rows
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[4][32 * DV];  // each wave's V rows
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -331,34 +340,55 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
   // are read back as the B operand of dP: registers for both would not fit. Dims at and
   // beyond D are zero in the slice (the dO tile's padding dims are not).
   const int dchunks = D >> 3;
+  constexpr bool NARROW = DV < DP;
+  const int Dv = NARROW ? p.Dv : D;
+  const int dvchunks = Dv >> 3;
   u32x4 kreg[S::KS];
   load_row_operand<DP>(p.k + b * p.k_sb + hk * p.k_sh +
                            static_cast<int64_t>(min(key, p.Skv - 1)) * p.k_ss, D, g, kreg);
   if (wave_live) {
     const uint16_t* vb = p.v + b * p.v_sb + hk * p.v_sh + static_cast<int64_t>(kw0) * p.v_ss;
 #pragma unroll
-    for (int j = 0; j < 32 * S::CPR / 64; ++j) {
+    for (int j = 0; j < 32 * SV::CPR / 64; ++j) {
       const int pos = j * 64 + lane;
-      const int row = pos / S::CPR;
-      const int cq = (pos - row * S::CPR) ^ bswz<DP>(row);
+      const int row = pos / SV::CPR;
+      const int cq = (pos - row * SV::CPR) ^ bswz<DV>(row);
       const int rr = min(row, p.Skv - 1 - kw0);
       u32x4 val = {0u, 0u, 0u, 0u};
-      if (cq < dchunks) val = *reinterpret_cast<const u32x4*>(vb + static_cast<int64_t>(rr) * p.v_ss + 8 * cq);
+      if (cq < dvchunks) val = *reinterpret_cast<const u32x4*>(vb + static_cast<int64_t>(rr) * p.v_ss + 8 * cq);
       *reinterpret_cast<u32x4*>(&v_lds[wave][8 * pos]) = val;
     }
   }
   const uint16_t* vw = v_lds[wave];
 
   // Tile loads: load j of this thread fills chunk position P = (4j + wave) * 64 + lane;
-  // LDS (row, c) holds global chunk c ^ bswz(row), clamped below head_dim.
-  uint32_t q_off[LPT], do_off[LPT];
+  // LDS (row, c) holds global chunk c ^ bswz(row), clamped below head_dim (dO: below
+  // V's width).
+  uint32_t q_off[LPT], do_off[LPTV];
+  if constexpr (!NARROW) {
 #pragma unroll
-  for (int j = 0; j < LPT; ++j) {
-    const int pos = (4 * j + wave) * 64 + lane;
-    const int row = pos / S::CPR;
-    const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
-    q_off[j] = static_cast<uint32_t>(row * p.q_ss * 2 + cq * 16);
-    do_off[j] = static_cast<uint32_t>(row * p.do_ss * 2 + cq * 16);
+    for (int j = 0; j < LPT; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / S::CPR;
+      const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
+      q_off[j] = static_cast<uint32_t>(row * p.q_ss * 2 + cq * 16);
+      do_off[j] = static_cast<uint32_t>(row * p.do_ss * 2 + cq * 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / S::CPR;
+      const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
+      q_off[j] = static_cast<uint32_t>(row * p.q_ss * 2 + cq * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < LPTV; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / SV::CPR;
+      const int cq = min((pos - row * SV::CPR) ^ bswz<DV>(row), dvchunks - 1);
+      do_off[j] = static_cast<uint32_t>(row * p.do_ss * 2 + cq * 16);
+    }
   }
   // Tiles are visited q head by q head of the group, q tiles ascending within each.
   // The next tile to issue is tracked incrementally (head r of the group, tile index
@@ -386,7 +416,7 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
 #pragma unroll
       for (int j = 0; j < LPT; ++j) {
         load_lds16_async(is_qb, q_off[j], lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
-        load_lds16_async(is_db, do_off[j], lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+        if (j < LPTV) load_lds16_async(is_db, do_off[j], lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
       }
     } else {
       // rows past Sq re-read row Sq - 1: their lse2 is +inf, so P = dS = 0
@@ -395,9 +425,20 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
         const int row = ((4 * j + wave) * 64 + lane) / S::CPR;
         const int over = max(0, q0 + row - (Sq - 1));
         const uint32_t qback = static_cast<uint32_t>(over * p.q_ss * 2);
-        const uint32_t dback = static_cast<uint32_t>(over * p.do_ss * 2);
         load_lds16_async(is_qb, q_off[j] - qback, lds_addr(&q_lds[buf][(4 * j + wave) * 512]));
-        load_lds16_async(is_db, do_off[j] - dback, lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+        if constexpr (!NARROW) {
+          const uint32_t dback = static_cast<uint32_t>(over * p.do_ss * 2);
+          load_lds16_async(is_db, do_off[j] - dback, lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+        }
+      }
+      if constexpr (NARROW) {
+#pragma unroll
+        for (int j = 0; j < LPTV; ++j) {
+          const int row = ((4 * j + wave) * 64 + lane) / SV::CPR;
+          const int over = max(0, q0 + row - (Sq - 1));
+          const uint32_t dback = static_cast<uint32_t>(over * p.do_ss * 2);
+          load_lds16_async(is_db, do_off[j] - dback, lds_addr(&do_lds[buf][(4 * j + wave) * 512]));
+        }
       }
     }
     if (wave == 0) {
@@ -420,18 +461,22 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
   const int a_rd0 = row_rd0<DP>(lane);
   int t_lo0, t_hi0;
   tr_offsets<DP>(lane, t_lo0, t_hi0);
+  // the dO / V tiles' offsets (the same as Q's unless V is narrower)
+  const int a_rd0v = row_rd0<DV>(lane);
+  int tv_lo0, tv_hi0;
+  tr_offsets<DV>(lane, tv_lo0, tv_hi0);
 
-  f32x16 dkacc[S::DB], dvacc[S::DB];
+  f32x16 dkacc[S::DB], dvacc[SV::DB];
 #pragma unroll
   for (int db = 0; db < S::DB; ++db) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       dkacc[db][r] = 0.0f;
-      dvacc[db][r] = 0.0f;
+      if (db < SV::DB) dvacc[db][r] = 0.0f;
     }
     if constexpr (kBwdMinBlocks<DP> == 1) {
       pin_agpr(dkacc[db]);
-      pin_agpr(dvacc[db]);
+      if (db < SV::DB) pin_agpr(dvacc[db]);
     }
   }
 
@@ -454,6 +499,9 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
     const int a_rd = opaque(a_rd0);
     const int t_lo = opaque(t_lo0);
     const int t_hi = opaque(t_hi0);
+    const int a_rdv = NARROW ? opaque(a_rd0v) : a_rd;
+    const int tv_lo = NARROW ? opaque(tv_lo0) : t_lo;
+    const int tv_hi = NARROW ? opaque(tv_hi0) : t_hi;
 
     f32x16 sacc, dpacc;
 #pragma unroll
@@ -461,23 +509,24 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
       sacc[r] = 0.0f;
       dpacc[r] = 0.0f;
     }
-    // operands one k-step ahead of the MFMAs that consume them
+    // operands one k-step ahead of the MFMAs that consume them (dP runs over V's
+    // SV::KS k-steps, S over head_dim's S::KS)
     u32x4 aq = *reinterpret_cast<const u32x4*>(ql + row_rd<DP>(a_rd, 0));
-    u32x4 ad = *reinterpret_cast<const u32x4*>(dl + row_rd<DP>(a_rd, 0));
-    u32x4 bv = *reinterpret_cast<const u32x4*>(vw + row_rd<DP>(a_rd, 0));
+    u32x4 ad = *reinterpret_cast<const u32x4*>(dl + row_rd<DV>(a_rdv, 0));
+    u32x4 bv = *reinterpret_cast<const u32x4*>(vw + row_rd<DV>(a_rdv, 0));
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
       u32x4 aq_n, ad_n, bv_n;
-      if (ks + 1 < S::KS) {
-        aq_n = *reinterpret_cast<const u32x4*>(ql + row_rd<DP>(a_rd, ks + 1));
-        ad_n = *reinterpret_cast<const u32x4*>(dl + row_rd<DP>(a_rd, ks + 1));
-        bv_n = *reinterpret_cast<const u32x4*>(vw + row_rd<DP>(a_rd, ks + 1));
+      if (ks + 1 < S::KS) aq_n = *reinterpret_cast<const u32x4*>(ql + row_rd<DP>(a_rd, ks + 1));
+      if (ks + 1 < SV::KS) {
+        ad_n = *reinterpret_cast<const u32x4*>(dl + row_rd<DV>(a_rdv, ks + 1));
+        bv_n = *reinterpret_cast<const u32x4*>(vw + row_rd<DV>(a_rdv, ks + 1));
       }
       __builtin_amdgcn_sched_barrier(0);
       sacc = E::mfma32(aq, kreg[ks], sacc);
-      dpacc = E::mfma32(ad, bv, dpacc);
-      if (ks + 1 < S::KS) {
-        aq = aq_n;
+      if (ks < SV::KS) dpacc = E::mfma32(ad, bv, dpacc);
+      if (ks + 1 < S::KS) aq = aq_n;
+      if (ks + 1 < SV::KS) {
         ad = ad_n;
         bv = bv_n;
       }
@@ -528,9 +577,10 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
                         E::pack2(dsv[e0 + 4], dsv[e0 + 5]), E::pack2(dsv[e0 + 6], dsv[e0 + 7])};
 #pragma unroll
       for (int db = 0; db < S::DB; ++db) {
-        const u32x4 ado = tr_operand<DP>(dl + 16 * cc * DP, t_lo, t_hi, db);
+        u32x4 ado;
+        if (db < SV::DB) ado = tr_operand<DV>(dl + 16 * cc * DV, tv_lo, tv_hi, db);
         const u32x4 aq = tr_operand<DP>(ql + 16 * cc * DP, t_lo, t_hi, db);
-        dvacc[db] = E::mfma32(ado, bp, dvacc[db]);
+        if (db < SV::DB) dvacc[db] = E::mfma32(ado, bp, dvacc[db]);
         dkacc[db] = E::mfma32(aq, bs, dkacc[db]);
       }
     }
@@ -538,7 +588,7 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
 #pragma unroll
       for (int db = 0; db < S::DB; ++db) {
         pin_agpr(dkacc[db]);
-        pin_agpr(dvacc[db]);
+        if (db < SV::DB) pin_agpr(dvacc[db]);
       }
     }
   }
@@ -546,24 +596,27 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dkdv_kernel(c
   if (wave_live && key < p.Skv) {
     store_rows<Tag, DP>(p.dk + b * p.dk_sb + hk * p.dk_sh + static_cast<int64_t>(key) * p.dk_ss,
                         dkacc, p.scale, D, g);
-    store_rows<Tag, DP>(p.dv + b * p.dv_sb + hk * p.dv_sh + static_cast<int64_t>(key) * p.dv_ss,
-                        dvacc, 1.0f, D, g);
+    store_rows<Tag, DV>(p.dv + b * p.dv_sb + hk * p.dv_sh + static_cast<int64_t>(key) * p.dv_ss,
+                        dvacc, 1.0f, Dv, g);
   }
 }
 
 // ---------------------------------------------------------------------------------
 // 3. dQ: queries stationary.
 // ---------------------------------------------------------------------------------
-template <typename Tag, int DP, bool SOFTCAP>
+template <typename Tag, int DP, int DV, bool SOFTCAP>
 __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(const BwdParams p) {
-  using S = BShape<DP>;
+  using S = BShape<DP>;   // Q, K, dQ
+  using SV = BShape<DV>;  // dO, V (dP^T = V dO^T over V's dims)
   using E = Elem<Tag>;
   constexpr int BN = kKeyTile;
   constexpr int TILE = BN * DP;
+  constexpr int TILE_V = BN * DV;
   constexpr int LPT = BN * S::CPR / kThreads;
-  static_assert(BN * S::CPR % kThreads == 0, "tile must split evenly");
+  constexpr int LPTV = BN * SV::CPR / kThreads;
+  static_assert(BN * S::CPR % kThreads == 0 && BN * SV::CPR % kThreads == 0, "tile must split evenly");
   __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][TILE];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][TILE_V];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -602,25 +655,45 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
   const float lse2 = p.lse2[ws];
   const float di = p.di[ws];
 
-  u32x4 qreg[S::KS], doreg[S::KS];
+  constexpr bool NARROW = DV < DP;
+  const int Dv = NARROW ? p.Dv : D;
+  u32x4 qreg[S::KS], doreg[SV::KS];
   {
     const int qr = min(qrow, p.Sq - 1);
     load_row_operand<DP>(p.q + b * p.q_sb + h * p.q_sh + static_cast<int64_t>(qr) * p.q_ss, D, g, qreg);
-    load_row_operand<DP>(p.dout + b * p.do_sb + h * p.do_sh + static_cast<int64_t>(qr) * p.do_ss, D, g,
+    load_row_operand<DV>(p.dout + b * p.do_sb + h * p.do_sh + static_cast<int64_t>(qr) * p.do_ss, Dv, g,
                          doreg);
   }
 
   const char* kbytes = reinterpret_cast<const char*>(p.k + b * p.k_sb + hk * p.k_sh);
   const char* vbytes = reinterpret_cast<const char*>(p.v + b * p.v_sb + hk * p.v_sh);
   const int dchunks = D >> 3;
-  uint32_t k_off[LPT], v_off[LPT];
+  const int dvchunks = Dv >> 3;
+  uint32_t k_off[LPT], v_off[LPTV];
+  if constexpr (!NARROW) {
 #pragma unroll
-  for (int j = 0; j < LPT; ++j) {
-    const int pos = (4 * j + wave) * 64 + lane;
-    const int row = pos / S::CPR;
-    const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
-    k_off[j] = static_cast<uint32_t>(row * p.k_ss * 2 + cq * 16);
-    v_off[j] = static_cast<uint32_t>(row * p.v_ss * 2 + cq * 16);
+    for (int j = 0; j < LPT; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / S::CPR;
+      const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
+      k_off[j] = static_cast<uint32_t>(row * p.k_ss * 2 + cq * 16);
+      v_off[j] = static_cast<uint32_t>(row * p.v_ss * 2 + cq * 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / S::CPR;
+      const int cq = min((pos - row * S::CPR) ^ bswz<DP>(row), dchunks - 1);
+      k_off[j] = static_cast<uint32_t>(row * p.k_ss * 2 + cq * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < LPTV; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / SV::CPR;
+      const int cq = min((pos - row * SV::CPR) ^ bswz<DV>(row), dvchunks - 1);
+      v_off[j] = static_cast<uint32_t>(row * p.v_ss * 2 + cq * 16);
+    }
   }
   auto issue = [&](int t, int buf) {
     const int kt0 = t * BN;
@@ -630,7 +703,7 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
 #pragma unroll
       for (int j = 0; j < LPT; ++j) {
         load_lds16_async(kb, k_off[j], lds_addr(&k_lds[buf][(4 * j + wave) * 512]));
-        load_lds16_async(vb, v_off[j], lds_addr(&v_lds[buf][(4 * j + wave) * 512]));
+        if (j < LPTV) load_lds16_async(vb, v_off[j], lds_addr(&v_lds[buf][(4 * j + wave) * 512]));
       }
     } else {
       // rows past Skv re-read row Skv - 1 (masked below)
@@ -640,13 +713,25 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
         const int over = max(0, kt0 + row - (Skv - 1));
         load_lds16_async(kb, k_off[j] - static_cast<uint32_t>(over * p.k_ss * 2),
                          lds_addr(&k_lds[buf][(4 * j + wave) * 512]));
-        load_lds16_async(vb, v_off[j] - static_cast<uint32_t>(over * p.v_ss * 2),
-                         lds_addr(&v_lds[buf][(4 * j + wave) * 512]));
+        if constexpr (!NARROW) {
+          load_lds16_async(vb, v_off[j] - static_cast<uint32_t>(over * p.v_ss * 2),
+                           lds_addr(&v_lds[buf][(4 * j + wave) * 512]));
+        }
+      }
+      if constexpr (NARROW) {
+#pragma unroll
+        for (int j = 0; j < LPTV; ++j) {
+          const int row = ((4 * j + wave) * 64 + lane) / SV::CPR;
+          const int over = max(0, kt0 + row - (Skv - 1));
+          load_lds16_async(vb, v_off[j] - static_cast<uint32_t>(over * p.v_ss * 2),
+                           lds_addr(&v_lds[buf][(4 * j + wave) * 512]));
+        }
       }
     }
   };
 
   const int a_rd0 = row_rd0<DP>(lane);
+  const int a_rd0v = row_rd0<DV>(lane);
   int t_lo0, t_hi0;
   tr_offsets<DP>(lane, t_lo0, t_hi0);
 
@@ -671,6 +756,7 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
     const uint16_t* kl = k_lds[buf];
     const uint16_t* vl = v_lds[buf];
     const int a_rd = opaque(a_rd0);
+    const int a_rdv = NARROW ? opaque(a_rd0v) : a_rd;
     const int t_lo = opaque(t_lo0);
     const int t_hi = opaque(t_hi0);
 
@@ -688,9 +774,11 @@ __global__ __launch_bounds__(kThreads, kBwdMinBlocks<DP>) void bwd_dq_kernel(con
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const u32x4 ak = *reinterpret_cast<const u32x4*>(kl + row_rd<DP>(a_rd, ks) + nb * 32 * DP);
-        const u32x4 av = *reinterpret_cast<const u32x4*>(vl + row_rd<DP>(a_rd, ks) + nb * 32 * DP);
         sacc[nb] = E::mfma32(ak, qreg[ks], sacc[nb]);
-        dpacc[nb] = E::mfma32(av, doreg[ks], dpacc[nb]);
+        if (ks < SV::KS) {
+          const u32x4 av = *reinterpret_cast<const u32x4*>(vl + row_rd<DV>(a_rdv, ks) + nb * 32 * DV);
+          dpacc[nb] = E::mfma32(av, doreg[ks < SV::KS ? ks : 0], dpacc[nb]);
+        }
       }
     }
 
@@ -1362,12 +1450,12 @@ void launch_f32(const BwdParams& p, bool softcap, int grid_pre, hipStream_t s) {
   }
 }
 
-template <typename Tag, int DP, bool SOFTCAP>
+template <typename Tag, int DP, bool SOFTCAP, int DV = DP>
 void launch_main(const BwdParams& p, int grid_dkv, int grid_dq, hipStream_t s) {
   if (grid_dkv > 0) {
-    hipLaunchKernelGGL((bwd_dkdv_kernel<Tag, DP, SOFTCAP>), dim3(grid_dkv), dim3(kThreads), 0, s, p);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<Tag, DP, DV, SOFTCAP>), dim3(grid_dkv), dim3(kThreads), 0, s, p);
   }
-  hipLaunchKernelGGL((bwd_dq_kernel<Tag, DP, SOFTCAP>), dim3(grid_dq), dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((bwd_dq_kernel<Tag, DP, DV, SOFTCAP>), dim3(grid_dq), dim3(kThreads), 0, s, p);
 }
 
 template <typename Tag>
@@ -1381,8 +1469,13 @@ void launch_tag(const BwdParams& p, bool softcap, int grid_pre, int grid_dkv, in
     softcap ? launch_main<Tag, 128, true>(p, grid_dkv, grid_dq, s)
             : launch_main<Tag, 128, false>(p, grid_dkv, grid_dq, s);
   } else if (p.D <= 192) {
-    softcap ? launch_main<Tag, 192, true>(p, grid_dkv, grid_dq, s)
-            : launch_main<Tag, 192, false>(p, grid_dkv, grid_dq, s);
+    if (p.Dv <= 128) {  // V narrower than q / k (the MLA module's)
+      softcap ? launch_main<Tag, 192, true, 128>(p, grid_dkv, grid_dq, s)
+              : launch_main<Tag, 192, false, 128>(p, grid_dkv, grid_dq, s);
+    } else {
+      softcap ? launch_main<Tag, 192, true>(p, grid_dkv, grid_dq, s)
+              : launch_main<Tag, 192, false>(p, grid_dkv, grid_dq, s);
+    }
   } else {
     softcap ? launch_main<Tag, 256, true>(p, grid_dkv, grid_dq, s)
             : launch_main<Tag, 256, false>(p, grid_dkv, grid_dq, s);
@@ -1443,6 +1536,7 @@ int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream) {
   p.Sq = a.seqlen_q;
   p.Skv = a.seqlen_kv;
   p.D = a.head_dim;
+  p.Dv = a.v_head_dim > 0 ? a.v_head_dim : a.head_dim;
   p.q_offset = a.q_offset;
   p.causal = a.causal ? 1 : 0;
   p.window = clamp_window(a.window, a.q_offset, a.seqlen_q);

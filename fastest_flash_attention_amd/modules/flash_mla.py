@@ -114,15 +114,14 @@ class FastestFlashMLA(nn.Module):
         B, S, _ = x.shape
         use_causal = self.default_causal if causal is None else causal
         bs = block_size or self.block_size or None
+        # V at its own head_dim: the forward and the backward take a narrower V as
+        # zero-padded (the same O as with v_padded, its rope_dim tail 0; dV on V's dims)
+        # and skip the P V / dO V^T / dV work on the pad
+        q, k, v = self.project_qkv(x, pad_v=False)
         if self.training:
-            q, k, v_padded = self.project_qkv(x)
-            attn = fastest_flash_attn_func(q, k, v_padded, scale=self.scale, causal=use_causal,
+            attn = fastest_flash_attn_func(q, k, v, scale=self.scale, causal=use_causal,
                                            block_size=bs or 64)
         else:
-            # V at its own head_dim: the forward takes a narrower V as zero-padded (the
-            # same O as with v_padded, its rope_dim tail 0) and runs P V over the real
-            # dims only
-            q, k, v = self.project_qkv(x, pad_v=False)
             attn, _ = fastest_flash_attn_forward(q, k, v, scale=self.scale,
                                                  causal=use_causal, block_size=bs)
         return self.o_proj(attn.transpose(1, 2).contiguous().view(B, S, -1))

@@ -63,8 +63,11 @@ def fastest_flash_attn_backward(
         raise ValueError("q, k, v must be 3D [B, S, D] or 4D [B, H, S, D]")
     B, Hq, Sq, D = q.shape
     Bk, Hkv, Skv, _ = k.shape
-    if v.shape != k.shape or k.size(3) != D:
+    # v may be narrower than q / k (taken as zero-padded, as the forward takes it): dv
+    # then has v's dims
+    if v.shape[:3] != k.shape[:3] or k.size(3) != D or not 1 <= v.size(3) <= D:
         raise ValueError(f"k {tuple(k.shape)} / v {tuple(v.shape)} do not match q {tuple(q.shape)}")
+    Dv = v.size(3)
     if grad_output.shape != q.shape or output.shape != q.shape:
         raise ValueError("grad_output and output must have q's shape")
     if tuple(lse.shape) != (B, Hq, Sq, 1):
@@ -95,15 +98,20 @@ def fastest_flash_attn_backward(
 
     dev = q.device
     d_pad = (D + 7) // 8 * 8
+    # a narrower v runs natively where the library has kernels for it (16-bit inputs,
+    # head_dim 129..192, v dims <= 128 and a multiple of 8), zero-padded here otherwise
+    narrow_v = (Dv < d_pad and code != _lib.FFA_DTYPE_FP32 and 128 < d_pad <= 192
+                and Dv <= 128 and Dv % 8 == 0)
+    dv_pad = Dv if narrow_v else d_pad
     if Bk != B:
         k = k.expand(B, -1, -1, -1)
         v = v.expand(B, -1, -1, -1)
     do_c, q_c, o_c = (_conform(t, d_pad) for t in (grad_output, q, output))
-    k_c, v_c = (_conform(t, d_pad) for t in (k, v))
+    k_c, v_c = _conform(k, d_pad), _conform(v, dv_pad)
     lse_c = lse.to(torch.float32)
     dq = torch.empty((B, Hq, Sq, d_pad), dtype=dtype, device=dev)
     dk = torch.empty((B, Hkv, Skv, d_pad), dtype=dtype, device=dev)
-    dv = torch.empty((B, Hkv, Skv, d_pad), dtype=dtype, device=dev)
+    dv = torch.empty((B, Hkv, Skv, dv_pad), dtype=dtype, device=dev)
     if B == 0 or Sq == 0:
         dq.zero_()
         dk.zero_()
@@ -135,12 +143,15 @@ def fastest_flash_attn_backward(
         a.scale = float(scale)
         a.softcap = float(softcap) if softcap is not None else 0.0
         a.dtype = code
+        a.v_head_dim = Dv if narrow_v else 0
         stream = _lib.current_stream_handle(dev)
         with torch.cuda.device(dev):
             rc = lib.ffa_attn_bwd(ctypes.byref(a), ctypes.c_void_p(stream))
         _lib.check(rc)
     if d_pad != D:
-        dq, dk, dv = (t[..., :D].contiguous() for t in (dq, dk, dv))
+        dq, dk = (t[..., :D].contiguous() for t in (dq, dk))
+    if dv.size(-1) != Dv:
+        dv = dv[..., :Dv].contiguous()
     if Bk != B:
         dk = dk.sum(dim=0, keepdim=True, dtype=torch.float32).to(dtype)
         dv = dv.sum(dim=0, keepdim=True, dtype=torch.float32).to(dtype)

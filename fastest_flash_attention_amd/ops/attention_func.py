@@ -62,10 +62,8 @@ def fastest_flash_attn_func(
 ) -> torch.Tensor:
     """Differentiable-API forward (reference ops/attention_func.py:93-125). The extra
     trailing ``num_kv_heads`` lets GQA callers skip materialising repeated KV heads."""
-    if v.size(-1) < q.size(-1):
-        # a narrower v is taken as zero-padded, as the forward takes it; the pad's own
-        # backward returns dV on v's dims
-        v = torch.nn.functional.pad(v, (0, q.size(-1) - v.size(-1)))
+    # a v narrower than q / k is taken as zero-padded by the forward and the backward
+    # (dV has v's dims)
     return FastestFlashAttnFunc.apply(
         q, k, v, scale, causal, block_size, softcap, sliding_window, two_pass, num_kv_heads,
     )

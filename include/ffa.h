@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define FFA_ABI_VERSION 6
+#define FFA_ABI_VERSION 7
 
 typedef enum ffa_status {
   FFA_OK = 0,
@@ -387,6 +387,10 @@ typedef struct ffa_attn_bwd_args {
   float scale;              /* any finite value */
   float softcap;            /* <= 0: no softcap; else finite */
   int32_t dtype;            /* ffa_dtype */
+  int32_t v_head_dim;       /* 0 or head_dim: v and dv have head_dim dims. Otherwise v
+                               and dv have v_head_dim < head_dim dims, v taken as
+                               zero-padded to head_dim as in ffa_prefill_fwd (dout and o
+                               keep head_dim dims); the same support rule. */
 } ffa_attn_bwd_args;
 
 size_t ffa_attn_bwd_workspace_bytes(int32_t batch, int32_t heads_q, int32_t seqlen_q);

@@ -141,6 +141,51 @@ def test_backward_parity(case):
     _check(dv, rv, dt, f"{name} dv")
 
 
+# (name, B, Hq, Hkv, Sq, Skv, D, Dv, q_offset, kwargs, dtype): v narrower than q / k,
+# taken as zero-padded (the MLA module's V); head_dim 129..192 with Dv <= 128 (a
+# multiple of 8) runs the narrow-V kernels, the last two are zero-padded on the host
+NARROW_V = [
+    ("mla_causal", 1, 4, 4, 300, 300, 192, 128, 0, {"causal": True}, BF16),
+    ("mla_gqa_window_softcap", 2, 4, 2, 257, 257, 192, 128, 0,
+     {"causal": True, "sliding_window": 90, "softcap": 30.0}, BF16),
+    ("mla_noncausal_ragged", 1, 2, 2, 150, 211, 192, 128, 0, {}, BF16),
+    ("d136_dv64_fp16_qoffset", 1, 2, 1, 60, 190, 136, 64, 130, {"causal": True}, F16),
+    ("d160_dv120_window", 1, 2, 2, 140, 140, 160, 120, 0, {"sliding_window": 41}, BF16),
+    ("host_padded_d128_dv64", 1, 2, 2, 90, 90, 128, 64, 0, {"causal": True}, BF16),
+    ("host_padded_fp32", 1, 2, 2, 90, 90, 192, 128, 0, {"causal": True}, F32),
+]
+
+
+@pytest.mark.parametrize("case", NARROW_V, ids=[c[0] for c in NARROW_V])
+def test_backward_narrow_v(case):
+    require_gpu()
+    name, B, Hq, Hkv, Sq, Skv, D, Dv, off, kw, dt = case
+    q = seeded((B, Hq, Sq, D), dt, 61)
+    k = seeded((B, Hkv, Skv, D), dt, 62)
+    v = seeded((B, Hkv, Skv, Dv), dt, 63)
+    do = seeded((B, Hq, Sq, D), dt, 64)
+    vp = torch.nn.functional.pad(v, (0, D - Dv))
+    scale = 1.0 / math.sqrt(D)
+    causal = kw.get("causal", False)
+    window = kw.get("sliding_window")
+    softcap = kw.get("softcap")
+    o32, lse = _oracle_forward(q, k, vp, scale=scale, causal=causal, window=window,
+                               softcap=softcap, q_offset=off)
+    o = torch.from_numpy(o32).to(dt)
+    say(f"backward narrow v {name} B{B} Hq{Hq} Hkv{Hkv} Sq{Sq} Skv{Skv} D{D} Dv{Dv} off{off} {kw} {dt}")
+    dq, dk, dv = ffa.fastest_flash_attn_backward(
+        do.cuda(), q.cuda(), k.cuda(), v.cuda(), o.cuda(), torch.from_numpy(lse).cuda(),
+        scale=scale, causal=causal, softcap=softcap, sliding_window=window, q_offset=off)
+    torch.cuda.synchronize()
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+    rq, rk, rv = rb.backward(np32(do), np32(q), np32(k), np32(vp), np32(o), lse, scale=scale,
+                             causal=causal, softcap=softcap, sliding_window=window,
+                             q_offset=off)
+    _check(dq, rq, dt, f"{name} dq")
+    _check(dk, rk, dt, f"{name} dk")
+    _check(dv, rv[..., :Dv], dt, f"{name} dv")
+
+
 @pytest.mark.parametrize("dt", [BF16, F32], ids=["bf16", "fp32"])
 def test_backward_deterministic(dt):
     """No atomics: two calls give bit-identical gradients (fp32: the four waves' partial
@@ -199,9 +244,9 @@ def test_autograd_func_gqa_matches_oracle():
 
 
 def test_autograd_func_narrow_v():
-    """fastest_flash_attn_func with V narrower than q / k (the MLA shape: 192 / 128) is
-    the zero-padded-V call: the same output and dQ / dK bit for bit, and dV is the padded
-    call's dV on V's own dims."""
+    """fastest_flash_attn_func with V narrower than q / k (the MLA shape: 192 / 128)
+    against the same call on the zero-padded V: the output and dQ / dK agree to the
+    kernels' rounding (other key tiles), and dV is the padded call's dV on V's dims."""
     require_gpu()
     B, H, S, D, Dv = 1, 4, 200, 192, 128
     q = seeded((B, H, S, D), BF16, 41).cuda()
@@ -217,9 +262,12 @@ def test_autograd_func_narrow_v():
         grads.append((out.detach(), qa.grad, ka.grad, va.grad))
     torch.cuda.synchronize()
     (o1, dq1, dk1, dv1), (o2, dq2, dk2, dv2) = grads
-    assert dv1.shape == v.shape
-    assert torch.equal(o1, o2) and torch.equal(dq1, dq2) and torch.equal(dk1, dk2)
-    assert torch.equal(dv1, dv2[..., :Dv])
+    assert dv1.shape == v.shape and torch.all(o1[..., Dv:] == 0)
+    for what, x, y in (("O", o1, o2), ("dQ", dq1, dq2), ("dK", dk1, dk2),
+                       ("dV", dv1, dv2[..., :Dv])):
+        d = (x.float() - y.float()).abs()
+        ref = y.float().abs().max().item()
+        assert d.max().item() <= 2e-2 * max(ref, 1.0), (what, d.max().item(), ref)
 
 
 def test_autograd_func_fp32_matches_oracle():

@@ -462,3 +462,16 @@ def test_host_layer_narrow_v():
     assert af.build_prefill_args(r, out, None, _lib.FFA_DTYPE_BF16).v_head_dim == 0
     with pytest.raises(ValueError):
         af.resolve_forward_args(q[..., :64], q[..., :64], v)  # v wider than q
+
+
+def test_abi_bwd_narrow_v_contract(lib):
+    """The backward takes a narrower V under the forward's rule, checked before any
+    HIP call."""
+    bw = _lib.AttnBwdArgs()
+    bw.dtype, bw.head_dim, bw.batch, bw.heads_q, bw.heads_kv = 0, 128, 1, 4, 2
+    bw.v_head_dim = 64
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -3  # only head_dim 129..192
+    bw.head_dim, bw.v_head_dim = 192, 100
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -4  # a multiple of 8
+    bw.v_head_dim, bw.dtype = 128, 2
+    assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -3  # 16-bit inputs only
