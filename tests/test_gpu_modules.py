@@ -3,13 +3,16 @@
 from __future__ import annotations
 
 import copy
+import math
 
+import numpy as np
 import pytest
 import torch
 
 import fastest_flash_attention_amd as ffa
 from fastest_flash_attention_amd.utils import repeat_kv
-from tests.gpu_util import require_gpu, say
+from oracle import reference_forward as rf
+from tests.gpu_util import np32, require_gpu, say
 
 pytestmark = pytest.mark.gpu
 
@@ -161,3 +164,51 @@ def test_mla_training_mode_backward_d192():
         print(f"  {name}: max err {err.max():.3e} (ref max {want.abs().max():.3e})", flush=True)
         assert err.max() <= 5e-2 * want.abs().max(), (name, err.max(), want.abs().max())
         assert err.mean() <= 2e-2 * want.abs().mean(), (name, err.mean(), want.abs().mean())
+
+
+def _close(name, got, want):
+    got = got.detach().float().cpu()
+    want = want.detach().float()
+    err = (got - want).abs()
+    print(f"  {name}: max err {err.max():.3e} (ref max {want.abs().max():.3e})", flush=True)
+    assert err.max() <= 5e-2 * want.abs().max(), (name, err.max(), want.abs().max())
+    assert err.mean() <= 2e-2 * want.abs().mean(), (name, err.mean(), want.abs().mean())
+
+
+def test_eval_modules_match_fp32_restatement():
+    """Eval mode of the three modules against an fp32 CPU restatement that shares no GPU
+    code: the module's own projections (and RoPE) on an fp32 copy of its weights, the
+    attention through the oracle (the reference dispatcher and CPU kernel, with its
+    softcap / window / GQA semantics), the output projection."""
+    require_gpu()
+    torch.manual_seed(5)
+    B, S = 2, 77
+    cases = [
+        ("MHA", ffa.FastestFlashMHA(hidden_size=256, num_heads=4, causal=True), {"causal": True}),
+        ("GQA", ffa.FastestFlashGQA(hidden_size=256, num_heads=8, num_kv_heads=2, causal=True,
+                                    softcap=30.0, sliding_window=40),
+         {"causal": True, "softcap": 30.0, "sliding_window": 40, "num_kv_heads": 2}),
+        ("MLA", ffa.FastestFlashMLA(hidden_size=256, num_heads=2, head_dim=128, latent_dim=64,
+                                    rope_dim=64), {"causal": True}),
+    ]
+    for name, m, kw in cases:
+        m = m.cuda().to(torch.bfloat16).eval()
+        x = torch.randn(B, S, 256, device="cuda").to(torch.bfloat16)
+        say(f"module {name} eval vs fp32 restatement")
+        with torch.no_grad():
+            out = m(x)
+            mr = copy.deepcopy(m).float().cpu()
+            xr = x.float().cpu()
+            if name == "MLA":
+                q, k, v = mr.project_qkv(xr)  # V zero-padded, as the reference builds it
+                scale = mr.scale
+            else:
+                Hkv = kw.get("num_kv_heads", mr.num_heads)
+                q = mr.q_proj(xr).view(B, S, mr.num_heads, mr.head_dim).transpose(1, 2)
+                k = mr.k_proj(xr).view(B, S, Hkv, mr.head_dim).transpose(1, 2)
+                v = mr.v_proj(xr).view(B, S, Hkv, mr.head_dim).transpose(1, 2)
+                scale = getattr(mr, "scale", 1.0 / math.sqrt(mr.head_dim))
+            a, _ = rf.forward(np32(q), np32(k), np32(v), scale=scale, return_lse=True, **kw)
+            ref = mr.o_proj(torch.from_numpy(np.ascontiguousarray(a)).transpose(1, 2).reshape(B, S, -1))
+        torch.cuda.synchronize()
+        _close(f"{name} out", out, ref)
