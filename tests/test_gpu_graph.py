@@ -47,6 +47,38 @@ def test_prefill_graph_replays_match_eager():
         assert torch.equal(call.lse.reshape(lse_ref.shape), lse_ref), f"replay {rep}: LSE differs"
 
 
+def test_prefill_graph_narrow_v_block_mask():
+    """A captured narrow-V prefill (head_dim 192 over a 128-dim V) with a block mask: the
+    launch carries dynamic LDS for the mask's tile list; replays equal eager calls."""
+    require_gpu()
+    B, H, S, D, Dv, bs = 1, 4, 260, 192, 128, 32
+    q = seeded((B, H, S, D), BF16, 81).cuda()
+    k = seeded((B, H, S, D), BF16, 82).cuda()
+    v = seeded((B, H, S, Dv), BF16, 83).cuda()
+    gen = torch.Generator().manual_seed(84)
+    n = (S + bs - 1) // bs
+    bm = torch.rand(n, n, generator=gen) < 0.6
+    kw = dict(causal=True, block_size=bs, block_mask=bm, return_lse=True)
+    say("prefill graph capture, narrow v + block mask")
+    call = prepare_prefill(q, k, v, **kw)
+    assert call.args.v_head_dim == Dv and call.args.block_key_mask
+    launch_prefill(call)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch_prefill(call)
+    for rep in range(3):
+        g2 = torch.Generator().manual_seed(200 + rep)
+        q.copy_(torch.randn(q.shape, generator=g2).to(BF16))
+        call.out.fill_(float("nan"))
+        call.lse.fill_(float("nan"))
+        graph.replay()
+        o_ref, lse_ref = ffa.fastest_flash_attn_forward(q, k, v, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(call.out.reshape(o_ref.shape), o_ref), f"replay {rep}: O differs from eager"
+        assert torch.equal(call.lse.reshape(lse_ref.shape), lse_ref), f"replay {rep}: LSE differs"
+
+
 def test_mla_decode_graph_replays_match_eager():
     require_gpu()
     B, H, L, lat, R, P = 5, 32, 700, 512, 64, 64
