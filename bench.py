@@ -122,18 +122,26 @@ def blas_threads() -> int:
 PROFILES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles")
 
 
-def profiled_traffic(summary: str):
+def profiled_traffic(summary: str, key: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch of a kernel as measured by the committed rocprofv3 PMC
-    summary ``profiles/<summary>`` (line ``traffic_bytes_per_launch: N``: FETCH_SIZE and
-    WRITE_SIZE per dispatch, each scaled by its calibration factor), or None."""
+    summary ``profiles/<summary>`` (line ``<key>: N``: FETCH_SIZE and WRITE_SIZE per
+    dispatch, each scaled by its calibration factor), or None."""
     try:
         with open(os.path.join(PROFILES, summary)) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return int(line.split(":", 1)[1].strip())
     except OSError:
         return None
     return None
+
+
+def cpu_threads() -> dict:
+    """Host thread counts reported beside every CPU figure."""
+    import torch
+
+    return {"os_cpu_count": os.cpu_count(), "torch_num_threads": torch.get_num_threads(),
+            "blas_threads": blas_threads()}
 
 
 def cpu_baseline_prefill(cfg: dict, q, k, v, budget_s: float) -> dict:
@@ -167,6 +175,7 @@ def cpu_baseline_prefill(cfg: dict, q, k, v, budget_s: float) -> dict:
         "value": flops / secs / 1e12,
         "unit": "TFLOP/s",
         "cores": blas_threads(),
+        **cpu_threads(),
         "kind": "port",
         "sample": (f"oracle/reference_forward.flash_attn_cpu_forward (numpy fp32, the "
                    f"reference CPU algorithm) on batch 0, heads 0..{heads - 1} "
@@ -258,13 +267,83 @@ def bench_backward(steps: int, warmup: int):
         "flops": flops,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
-                     "traffic": profiled_traffic("bwd_dkdv_kernel_north_star.md")},
+                     # the whole step: preprocess + dK/dV + dQ kernels
+                     "traffic": profiled_traffic("bwd_dkdv_kernel_north_star.md",
+                                                 "step_traffic_bytes")},
         "config": {"workload": "north_star_backward", "batch": B, "heads": H, "seq_len": S,
                    "head_dim": D, "causal": True},
     }
 
 
-def bench_decode(steps: int, warmup: int):
+def cpu_baseline_decode(k_pages, v_pages, q, bt, lens, budget_s: float) -> dict:
+    """The reference CPU decode path on sequences 0, 1, ... of the same seeded cfg4
+    batch until the time budget is spent: ``get_kv`` (the per-page copy loop,
+    oracle/paged.gather_sequence, moving the pool's 16-bit words as they are) and the
+    one-token attention over the gathered K/V (bf16 -> fp32, repeat_kv, the reference
+    CPU kernel with the query at position L - 1: oracle/reference_forward). Timed
+    separately and together; GB/s on the same algorithmic bytes as the GPU leg."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import paged as opaged
+    from oracle import reference_forward as rf
+
+    B, Hq, D = q.shape
+    Hkv, P = k_pages.shape[1], k_pages.shape[2]
+    # the pools move to host memory once (16-bit words, as the reference's bf16 pool
+    # would hold them); the copy is not timed
+    kh = k_pages.view(torch.int16).cpu().numpy()
+    vh = v_pages.view(torch.int16).cpu().numpy()
+    qh = q.float().cpu().numpy()
+    bth = bt.cpu().numpy()
+    lens_h = [int(x) for x in lens.cpu()]
+
+    def f32(words):  # exact bf16 -> fp32 widening of the gathered words
+        return (words.astype(np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+    t_gather = t_attn = 0.0
+    nbytes = 0
+    n = 0
+    bs = None
+    while n < B and (n == 0 or t_gather + t_attn < budget_s):
+        L = lens_h[n]
+        pages = bth[n, :(L + P - 1) // P].tolist()
+        t = time.perf_counter()
+        kb, vb = opaged.gather_sequence(kh, vh, pages, L)
+        t_gather += time.perf_counter() - t
+        t = time.perf_counter()
+        kf = rf.repeat_kv(f32(kb)[None], Hq, Hkv)
+        vf = rf.repeat_kv(f32(vb)[None], Hq, Hkv)
+        bs = rf.auto_select_block_size(1, L, D)
+        rf.flash_attn_cpu_forward(qh[n][None, :, None, :], kf, vf, scale=1 / math.sqrt(D),
+                                  causal=True, block_q=bs, block_kv=bs, q_offset=L - 1,
+                                  return_lse=True)
+        t_attn += time.perf_counter() - t
+        nbytes += L * Hkv * D * 2 * 2 + 2 * Hq * D * 2 + Hq * 4 + len(pages) * 4 + 4
+        n += 1
+    total = t_gather + t_attn
+    return {
+        "value": nbytes / total / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        **cpu_threads(),
+        "kind": "port",
+        "gather_GBps": nbytes / t_gather / 1e9,
+        "attention_GBps": nbytes / t_attn / 1e9,
+        "gather_s": t_gather,
+        "attention_s": t_attn,
+        "sample": (f"sequences 0..{n - 1} of the {B}-sequence cfg4 batch ({sum(lens_h[:n])} "
+                   f"of {sum(lens_h)} tokens, {nbytes:.3e} B): oracle/paged.gather_sequence "
+                   f"(the reference get_kv page loop, numpy) then the one-token reference "
+                   f"CPU attention (oracle/reference_forward, fp32, block {bs} as the "
+                   f"reference dispatcher picks for the last sequence); gather "
+                   f"{t_gather:.2f} s + attention {t_attn:.2f} s; numpy copies and "
+                   f"per-tile products of one query row run on one thread"),
+    }
+
+
+def bench_decode(steps: int, warmup: int, cpu_budget: float = 0.0):
     import torch
 
     import fastest_flash_attention_amd as ffa
@@ -310,6 +389,8 @@ def bench_decode(steps: int, warmup: int):
         "config": {"workload": "cfg4_paged_decode", "batch": B, "heads_q": Hq, "heads_kv": Hkv,
                    "head_dim": D, "page_size": P, "context_lens": "U[512, 32768] seed 0",
                    "total_tokens": int(lens.sum())},
+        "cpu_baseline": (cpu_baseline_decode(k_pages, v_pages, q, btd, lensd, cpu_budget)
+                         if cpu_budget > 0 else None),
     }
 
 
@@ -380,7 +461,9 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-backward", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
-                    help="time budget of the CPU baseline sample (0 disables it)")
+                    help="time budget of the prefill CPU baseline sample (0 disables it)")
+    ap.add_argument("--cpu-decode-seconds", type=float, default=6.0,
+                    help="time budget of the decode CPU baseline sample (0 disables it)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="run one fp32 elementwise kernel over this many MiB first (a "
                          "known-size kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -409,7 +492,8 @@ def main() -> int:
     # The headline prefill leg runs last: the other legs bring the GPU out of idle first
     # (its clock ramps over ~0.1-0.3 s of load), so the headline's own W warm-up steps
     # are not also spent on the ramp.
-    dec = None if args.no_decode else bench_decode(args.steps, args.warmup)
+    dec = None if args.no_decode else bench_decode(args.steps, args.warmup,
+                                                   args.cpu_decode_seconds)
     mla = None if args.no_decode else bench_mla_decode(args.steps, args.warmup)
     bwd = None if args.no_backward else bench_backward(args.steps, args.warmup)
     pre = bench_prefill(args.workload, args.steps, args.warmup, args.cpu_seconds)

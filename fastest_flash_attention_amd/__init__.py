@@ -25,7 +25,7 @@ from .ops import (
 )
 from .utils import auto_select_block_size, check_hip_available, check_triton_available
 
-__version__ = "0.1.0"
+__version__ = "1.0.0"  # the reference package's version (its __init__.py:59): a drop-in
 
 __all__ = [
     "AttentionConfig",

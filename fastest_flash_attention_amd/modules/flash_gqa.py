@@ -4,6 +4,13 @@ Same interface and outputs as the reference. The reference materialises
 ``repeat_kv`` before calling the op (:102-103); here the KV heads are handed over
 unrepeated with ``num_kv_heads`` and the HIP kernel maps q head h to kv head
 ``h // (num_heads // num_kv_heads)`` — the identical head map without the copy.
+
+A ``kv_cache`` in the reference's layout holds ``num_heads`` heads (the reference
+concatenates it with the repeated K/V, :102-103,121-125 -> ops/attention_forward.py:82-89):
+then the S new K/V rows are repeated to ``num_heads`` as the reference repeats them and
+the op runs with one KV head per q head. A cache of ``num_kv_heads`` heads is accepted
+too (an extension: it is what the unrepeated path concatenates with, and it is
+``num_heads // num_kv_heads`` times smaller).
 """
 
 from __future__ import annotations
@@ -16,6 +23,7 @@ import torch.nn as nn
 
 from ..ops.attention_forward import fastest_flash_attn_forward
 from ..ops.attention_func import fastest_flash_attn_func
+from ..utils import repeat_kv
 
 
 class FastestFlashGQA(nn.Module):
@@ -55,7 +63,10 @@ class FastestFlashGQA(nn.Module):
         kv_cache: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
         return_lse: bool = False,
     ) -> torch.Tensor | Tuple[torch.Tensor, torch.Tensor]:
-        """x: [B, S, hidden] -> [B, S, hidden]. A kv_cache holds num_kv_heads heads."""
+        """x: [B, S, hidden] -> [B, S, hidden] (or (out, lse) with return_lse).
+
+        ``kv_cache = (K_c, V_c)`` is ``[B, num_heads, S_c, head_dim]`` as in the
+        reference, or ``[B, num_kv_heads, S_c, head_dim]``."""
         B, S, _ = x.shape
         use_causal = self.default_causal if causal is None else causal
         bs = block_size or self.block_size or None
@@ -70,15 +81,26 @@ class FastestFlashGQA(nn.Module):
             )
             lse = None
         else:
+            kv_heads = self.num_kv_heads
+            if kv_cache is not None and self._cache_heads(kv_cache) == self.num_heads != kv_heads:
+                # the reference layout: its K/V are repeated before the concatenation
+                k = repeat_kv(k, self.num_heads, kv_heads)
+                v = repeat_kv(v, self.num_heads, kv_heads)
+                kv_heads = None
             attn, lse = fastest_flash_attn_forward(
                 q, k, v, scale=self.scale, causal=use_causal, block_size=bs,
                 softcap=self.softcap, sliding_window=self.sliding_window,
-                num_kv_heads=self.num_kv_heads, kv_cache=kv_cache, return_lse=return_lse,
+                num_kv_heads=kv_heads, kv_cache=kv_cache, return_lse=return_lse,
             )
         out = self.o_proj(attn.transpose(1, 2).contiguous().view(B, S, -1))
         if return_lse:
             return out, lse
         return out
+
+    @staticmethod
+    def _cache_heads(kv_cache) -> int:
+        k_cache = kv_cache[0]
+        return 1 if k_cache.dim() == 3 else k_cache.size(1)
 
     def extra_repr(self) -> str:
         return (

@@ -71,14 +71,14 @@ def _paged_decode_fp32(q3, k_pages, v_pages, block_tables, context_lens, scale, 
     ``ffa_prefill_fwd`` on the fp32 MFMA kernel with the query at position L - 1 (the
     reference's get_kv + forward, ops/kv_cache.py:208-232, in fp32 as it computes).
     Two launches per sequence instead of the batched split-K kernels, which take
-    16-bit pools; page ids are always checked (IndexError)."""
+    16-bit pools; page ids are always checked (IndexError). The caller has checked the
+    pools' contiguity, the tables' dtype and their width against max_context_len."""
     B, Hq, D = q3.shape
     P_total, Hkv, page_size, _ = k_pages.shape
-    lens = context_lens.to(torch.int64).clamp(min=0).tolist()
-    if max_context_len is not None:
-        lens = [min(n, int(max_context_len)) for n in lens]
-    bt = block_tables.to(torch.int32).contiguous()
-    check_page_ids(bt, context_lens, page_size, P_total, max(lens + [0]))
+    lens = [min(n, int(max_context_len))
+            for n in context_lens.to(torch.int64).clamp(min=0).tolist()]
+    bt = block_tables  # int32, contiguous, wide enough for max_context_len (checked)
+    check_page_ids(bt, context_lens, page_size, P_total, int(max_context_len))
     out = torch.zeros((B, Hq, D), dtype=torch.float32, device=q3.device)
     lse = (torch.full((B, Hq), float("-inf"), dtype=torch.float32, device=q3.device)
            if return_lse else None)
@@ -144,6 +144,11 @@ def fastest_flash_paged_decode(
     with ``check_block_tables=True`` they raise IndexError instead, as the reference's
     page indexing does (ops/kv_cache.py:226-227).
 
+    fp32 pools (the reference test's dtype) take another route: per sequence, a gather
+    of its pages and the fp32 prefill kernel, two launches and a host sync per
+    sequence. On that route page ids are always checked (IndexError, whatever
+    ``check_block_tables`` says), and ``tokens_per_split`` and ``workspace`` are unused.
+
     q: ``[B, Hq, D]`` or ``[B, Hq, 1, D]``; k_pages/v_pages: ``[P, Hkv, page_size, D]``
     (PagedKVCache layout); block_tables: int32 ``[B, max_blocks]``; context_lens: int32
     ``[B]``. Sequence b attends to its first ``context_lens[b]`` tokens with the query at
@@ -170,6 +175,23 @@ def fastest_flash_paged_decode(
         raise ValueError(f"head_dim mismatch: q {D}, pages {Dk}")
     if Hq % Hkv != 0:
         raise ValueError(f"heads_q {Hq} is not a multiple of heads_kv {Hkv}")
+    if not (q3.dtype == k_pages.dtype == v_pages.dtype):
+        raise TypeError("q and the page pools must share a dtype")
+    # checks every pool dtype shares: the kernels (and the fp32 route's gather) index
+    # the pools as contiguous and read ceil(L / page_size) entries of a table row
+    if not (k_pages.is_contiguous() and v_pages.is_contiguous()):
+        raise ValueError("page pools must be contiguous")
+    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
+        raise TypeError("block_tables and context_lens must be int32")
+    if (block_tables.dim() != 2 or block_tables.size(0) < B or context_lens.dim() != 1
+            or context_lens.size(0) < B):
+        raise ValueError("block_tables must be [B, max_blocks] and context_lens [B]")
+    block_tables = block_tables.contiguous()
+    context_lens = context_lens.contiguous()
+    if max_context_len is None:
+        max_context_len = int(context_lens.max().item()) if B > 0 else 0
+    if block_tables.size(1) * page_size < max_context_len:
+        raise ValueError("block_tables has fewer columns than max_context_len needs")
     for name, t in (("q", q3), ("k_pages", k_pages), ("v_pages", v_pages),
                     ("block_tables", block_tables), ("context_lens", context_lens)):
         if t.device.type != "cuda":
@@ -177,8 +199,6 @@ def fastest_flash_paged_decode(
                 f"fastest_flash_attention_amd paged decode runs on ROCm tensors only; "
                 f"{name} is on {t.device}"
             )
-    if not (q3.dtype == k_pages.dtype == v_pages.dtype):
-        raise TypeError("q and the page pools must share a dtype")
     if q3.dtype == torch.float32:
         out, lse = _paged_decode_fp32(q3, k_pages, v_pages, block_tables, context_lens,
                                       scale, softcap, sliding_window, return_lse,
@@ -191,18 +211,8 @@ def fastest_flash_paged_decode(
     code = _lib.dtype_code(q3.dtype)
     if D % 8 != 0:
         raise ValueError(f"paged decode needs head_dim % 8 == 0 (got {D})")
-    if not (k_pages.is_contiguous() and v_pages.is_contiguous()):
-        raise ValueError("page pools must be contiguous")
-    if block_tables.dtype != torch.int32 or context_lens.dtype != torch.int32:
-        raise TypeError("block_tables and context_lens must be int32")
-    block_tables = block_tables.contiguous()
-    context_lens = context_lens.contiguous()
     if q3.stride(-1) != 1 or q3.data_ptr() % 16 or q3.stride(0) % 8 or q3.stride(1) % 8:
         q3 = q3.contiguous() if not q3.is_contiguous() else q3.clone()
-    if max_context_len is None:
-        max_context_len = int(context_lens.max().item()) if B > 0 else 0
-    if block_tables.size(1) * page_size < max_context_len:
-        raise ValueError("block_tables has fewer columns than max_context_len needs")
     if check_block_tables:
         check_page_ids(block_tables, context_lens, page_size, P_total, max_context_len)
     if scale is None:

@@ -53,7 +53,9 @@ def mla_decode_workspace_bytes(batch: int, heads_q: int, dim_v: int, max_context
 class MlaDecodeCall:
     """A fully resolved MLA decode launch: the ABI struct plus the tensors it points to
     (kept alive with it). ``launch_mla_decode`` runs it on the current stream; a serving
-    loop that refills q / context_lens in place can launch the same call every step."""
+    loop that refills q / context_lens in place can launch the same call every step, as
+    long as every length stays within the ``max_context_len`` it was prepared with
+    (longer sequences are cut to that many tokens)."""
 
     args: _lib.MlaDecodeArgs
     q: torch.Tensor
@@ -78,7 +80,17 @@ def prepare_mla_decode(
     out: Optional[torch.Tensor] = None,
 ) -> MlaDecodeCall:
     """Check the arguments of ``fastest_flash_mla_decode``, allocate outputs (or take
-    ``out``) and the workspace, build the ABI struct. Launches nothing."""
+    ``out``) and the workspace, build the ABI struct. Launches nothing.
+
+    ``max_context_len`` is required here: a call prepared once may be launched again
+    after ``context_lens`` has been refilled in place, and the prepared bound fixes the
+    split count, the workspace size and the table width the kernels may read. Every
+    later launch attends to the first ``min(context_lens[b], max_context_len)`` tokens
+    of sequence b, so a serving loop whose lengths grow passes the largest length it
+    will reach (and a block table that wide) or prepares the call again."""
+    if max_context_len is None:
+        raise ValueError("prepare_mla_decode needs an explicit max_context_len: it bounds "
+                         "every context length the prepared call will be launched with")
     if q.dim() != 3 or kv_pages.dim() != 3:
         raise ValueError("q must be [B, H, dim_v + 64] and kv_pages [num_pages, page_size, dim_v + 64]")
     B, H, dqk = q.shape
@@ -102,8 +114,9 @@ def prepare_mla_decode(
     context_lens = context_lens.contiguous()
     if q.stride(-1) != 1 or q.data_ptr() % 16 or q.stride(0) % 8 or q.stride(1) % 8:
         q = q.contiguous() if not q.is_contiguous() else q.clone()
-    if max_context_len is None:
-        max_context_len = int(context_lens.max().item()) if B > 0 else 0
+    max_context_len = int(max_context_len)
+    if max_context_len < 0:
+        raise ValueError("max_context_len must be >= 0")
     if block_tables.size(1) * page_size < max_context_len:
         raise ValueError("block_tables has fewer columns than max_context_len needs")
     if check_block_tables:
@@ -183,6 +196,9 @@ def fastest_flash_mla_decode(
     ``[B, max_blocks]``; context_lens int32 ``[B]``. Sequence b attends to its first
     ``context_lens[b]`` tokens. Returns ``(o_lat [B, H, dim_v], lse [B, H] or None)``.
     """
+    if max_context_len is None:
+        max_context_len = (int(context_lens.max().item())
+                           if context_lens.numel() > 0 and q.size(0) > 0 else 0)
     call = prepare_mla_decode(q, kv_pages, block_tables, context_lens, dim_v=dim_v,
                               scale=scale, return_lse=return_lse,
                               max_context_len=max_context_len,

@@ -277,7 +277,10 @@ int ffa_paged_decode_fwd(const ffa_paged_decode_args* args, void* stream);
  * partials there: calls that overlap on one GPU (other streams, other threads) race,
  * so the caller serialises them. Nothing in the array has to start at zero (each
  * call writes every partial it reads). The first call on a device looks up the
- * array's address on that device once.
+ * array's address on that device once (hipGetSymbolAddress): make that first call
+ * eagerly, outside HIP graph capture; later calls may be captured and replayed.
+ * The array is a standing cost: loading libffa.so reserves its 64 MiB on every GPU
+ * where the code object is loaded, whether or not this entry point is ever called.
  */
 #define FFA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int ffa_paged_decode_fwd_noalloc(const ffa_paged_decode_args* args, void* stream);

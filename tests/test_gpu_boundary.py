@@ -126,11 +126,15 @@ def test_decode_invalid_pages_are_excluded():
     assert_parity(o1, ro1, what="valid tables")
 
 
-def test_mla_decode_invalid_pages_are_excluded():
+@pytest.mark.parametrize("dim_v,P", [(512, 16), (512, 64), (256, 32)])
+def test_mla_decode_invalid_pages_are_excluded(dim_v, P):
+    """Page sizes that are multiples of 32 take the kernel's whole-tile page path (one
+    page id per 32-token tile); 16 takes the per-row path. Both exclude the tokens of
+    out-of-range ids."""
     require_gpu()
     g = torch.Generator().manual_seed(43)
-    H, dim_v, P, num_pages = 32, 512, 16, 30
-    lens = [200, 64, 5]
+    H, num_pages = 32, 30
+    lens = [200, 100, 5]
     pool = torch.randn(num_pages, P, dim_v + 64, generator=g).to(BF16)
     bt = torch.randint(0, num_pages, (3, 13), generator=g, dtype=torch.int32)
     bt[0, 3] = -2
@@ -138,7 +142,7 @@ def test_mla_decode_invalid_pages_are_excluded():
     bt[2, 0] = 12345
     q = torch.randn(3, H, dim_v + 64, generator=g).to(BF16)
     scale = 1 / math.sqrt(dim_v + 64)
-    say("mla decode invalid pages")
+    say(f"mla decode invalid pages dim_v {dim_v} page {P}")
     o, lse = ffa.fastest_flash_mla_decode(q.cuda(), pool.cuda(), bt.cuda(),
                                           torch.tensor(lens, dtype=torch.int32).cuda(),
                                           dim_v=dim_v, scale=scale, return_lse=True,

@@ -48,6 +48,7 @@ MLA_CASES = [
     (F16, 256, 16, 12, [130, 77, 5], 64),
     (BF16, 512, 8, 16, [1024, 3], 1024),
     (BF16, 256, 1, 1, [45, 9], 32),
+    (BF16, 256, 32, 32, [700, 64, 33, 1], None),  # whole-tile page path at dim_v 256
 ]
 
 
@@ -168,7 +169,10 @@ def test_prepared_mla_call_matches_one_shot():
     q, pool, bt, lens_t = _paged_case(21, lens, 16, 512, 32, BF16)
     q, pool, bt, lens_t = q.cuda(), pool.cuda(), bt.cuda(), lens_t.cuda()
     say("mla decode prepared call")
-    call = prepare_mla_decode(q, pool, bt, lens_t, dim_v=512, scale=0.06, return_lse=True)
+    with pytest.raises(ValueError, match="max_context_len"):
+        prepare_mla_decode(q, pool, bt, lens_t, dim_v=512, scale=0.06)
+    call = prepare_mla_decode(q, pool, bt, lens_t, dim_v=512, scale=0.06, return_lse=True,
+                              max_context_len=300)
     for seed in (0, 1):
         if seed:
             q.copy_(torch.randn(q.shape, generator=torch.Generator().manual_seed(seed)).to(BF16))
@@ -177,3 +181,13 @@ def test_prepared_mla_call_matches_one_shot():
                                               return_lse=True)
         torch.cuda.synchronize()
         assert torch.equal(call.out, o) and torch.equal(call.lse, lse)
+    # lengths refilled past the prepared bound: the documented limit, the first
+    # max_context_len tokens of the longer sequence
+    lens_t.copy_(torch.tensor([310, 45, 1], dtype=torch.int32))
+    launch_mla_decode(call)
+    torch.cuda.synchronize()
+    lens_t.copy_(torch.tensor([300, 45, 1], dtype=torch.int32))
+    o, lse = ffa.fastest_flash_mla_decode(q, pool, bt, lens_t, dim_v=512, scale=0.06,
+                                          return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(call.out, o) and torch.equal(call.lse, lse)

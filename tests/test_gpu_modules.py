@@ -212,3 +212,47 @@ def test_eval_modules_match_fp32_restatement():
             ref = mr.o_proj(torch.from_numpy(np.ascontiguousarray(a)).transpose(1, 2).reshape(B, S, -1))
         torch.cuda.synchronize()
         _close(f"{name} out", out, ref)
+
+
+@pytest.mark.parametrize("name", ["MHA", "GQA-ref-layout", "GQA-kv-heads"])
+def test_modules_with_kv_cache_match_oracle(name):
+    """Eval-mode MHA / GQA modules with a kv_cache (decode-style: a few new tokens after
+    a cached prefix) against the oracle's forward(..., kv_cache=...) fed the module's own
+    fp32 projections. The GQA module takes the reference's cache layout, num_heads heads
+    (ref modules/flash_gqa.py:101-125), and the num_kv_heads-head cache extension."""
+    require_gpu()
+    torch.manual_seed(12)
+    B, S, Sc, H, Hkv, D = 2, 3, 150, 8, 2, 64
+    hidden = H * D
+    if name == "MHA":
+        m = ffa.FastestFlashMHA(hidden_size=hidden, num_heads=H, causal=True)
+        Hc, kw = H, {}
+    else:
+        m = ffa.FastestFlashGQA(hidden_size=hidden, num_heads=H, num_kv_heads=Hkv, causal=True,
+                                softcap=30.0, sliding_window=100)
+        Hc = H if name == "GQA-ref-layout" else Hkv
+        kw = {"softcap": 30.0, "sliding_window": 100}
+    m = m.cuda().to(torch.bfloat16).eval()
+    x = torch.randn(B, S, hidden).to(torch.bfloat16)
+    kc = torch.randn(B, Hc, Sc, D).to(torch.bfloat16)
+    vc = torch.randn(B, Hc, Sc, D).to(torch.bfloat16)
+    say(f"module {name} with kv_cache")
+    with torch.no_grad():
+        out, lse = m(x.cuda(), kv_cache=(kc.cuda(), vc.cuda()), return_lse=True)
+        torch.cuda.synchronize()
+        mr = copy.deepcopy(m).float().cpu()
+        xr = x.float()
+        q = mr.q_proj(xr).view(B, S, H, D).transpose(1, 2)
+        hk = H if name == "MHA" else Hkv
+        k = mr.k_proj(xr).view(B, S, hk, D).transpose(1, 2)
+        v = mr.v_proj(xr).view(B, S, hk, D).transpose(1, 2)
+        if name == "GQA-ref-layout":  # the reference module repeats, then the op concatenates
+            k, v = repeat_kv(k, H, Hkv), repeat_kv(v, H, Hkv)
+        okw = dict(kw)
+        if name == "GQA-kv-heads":
+            okw["num_kv_heads"] = Hkv
+        a, l_ref = rf.forward(np32(q), np32(k), np32(v), scale=mr.scale, causal=True,
+                              kv_cache=(np32(kc), np32(vc)), return_lse=True, **okw)
+        ref = mr.o_proj(torch.from_numpy(np.ascontiguousarray(a)).transpose(1, 2).reshape(B, S, -1))
+    _close(f"{name} out", out, ref)
+    assert np.abs(np32(lse) - l_ref).max() <= 1e-2, np.abs(np32(lse) - l_ref).max()

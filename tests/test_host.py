@@ -475,3 +475,90 @@ def test_abi_bwd_narrow_v_contract(lib):
     assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -4  # a multiple of 8
     bw.v_head_dim, bw.dtype = 128, 2
     assert lib.ffa_attn_bwd(ctypes.byref(bw), None) == -3  # 16-bit inputs only
+
+
+# ---------------------------------------------------------------------------------
+# Module kv_cache contract (reference modules/flash_gqa.py:101-125,
+# ops/attention_forward.py:82-96): the op is replaced by the oracle on the CPU so that
+# only the module's own argument plumbing is under test
+# ---------------------------------------------------------------------------------
+
+def _oracle_op(q, k, v, **kw):
+    from oracle import reference_forward as rf
+
+    kc = kw.pop("kv_cache", None)
+    if kc is not None:
+        kc = tuple(t.detach().float().numpy() for t in kc)
+    o, lse = rf.forward(q.detach().float().numpy(), k.detach().float().numpy(),
+                        v.detach().float().numpy(), kv_cache=kc, **kw)
+    return torch.from_numpy(np.ascontiguousarray(o)), (
+        None if lse is None else torch.from_numpy(np.ascontiguousarray(lse)))
+
+
+@pytest.mark.parametrize("cache_heads", ["num_heads", "num_kv_heads"])
+def test_gqa_module_kv_cache_layouts(monkeypatch, cache_heads):
+    from fastest_flash_attention_amd.modules import flash_gqa
+    from oracle import reference_forward as rf
+
+    monkeypatch.setattr(flash_gqa, "fastest_flash_attn_forward", _oracle_op)
+    torch.manual_seed(11)
+    B, S, Sc, H, Hkv, D = 2, 5, 23, 8, 2, 16
+    m = ffa.FastestFlashGQA(hidden_size=H * D, num_heads=H, num_kv_heads=Hkv, causal=True,
+                            softcap=20.0, sliding_window=12).eval()
+    x = torch.randn(B, S, H * D)
+    hc = H if cache_heads == "num_heads" else Hkv
+    kc, vc = torch.randn(B, hc, Sc, D), torch.randn(B, hc, Sc, D)
+    with torch.no_grad():
+        out, lse = m(x, kv_cache=(kc, vc), return_lse=True)
+        # the reference module's statements: repeat the new K/V, concatenate the cache
+        q = m.q_proj(x).view(B, S, H, D).transpose(1, 2)
+        k = m.k_proj(x).view(B, S, Hkv, D).transpose(1, 2)
+        v = m.v_proj(x).view(B, S, Hkv, D).transpose(1, 2)
+        if cache_heads == "num_heads":
+            k = torch.repeat_interleave(k, H // Hkv, dim=1)
+            v = torch.repeat_interleave(v, H // Hkv, dim=1)
+        else:  # the extension: the cache holds the unrepeated heads
+            kc = torch.repeat_interleave(kc, H // Hkv, dim=1)
+            vc = torch.repeat_interleave(vc, H // Hkv, dim=1)
+            k = torch.repeat_interleave(k, H // Hkv, dim=1)
+            v = torch.repeat_interleave(v, H // Hkv, dim=1)
+        a, l_ref = rf.forward(q.numpy(), k.numpy(), v.numpy(), scale=m.scale, causal=True,
+                              softcap=20.0, sliding_window=12,
+                              kv_cache=(kc.numpy(), vc.numpy()), return_lse=True)
+        ref = m.o_proj(torch.from_numpy(np.ascontiguousarray(a)).transpose(1, 2).reshape(B, S, -1))
+    assert torch.allclose(out, ref, atol=1e-5, rtol=1e-5)
+    assert np.allclose(lse.numpy(), l_ref, atol=1e-6)
+
+
+def test_gqa_module_rejects_other_cache_head_counts(monkeypatch):
+    from fastest_flash_attention_amd.modules import flash_gqa
+
+    monkeypatch.setattr(flash_gqa, "fastest_flash_attn_forward", _oracle_op)
+    m = ffa.FastestFlashGQA(hidden_size=64, num_heads=4, num_kv_heads=2).eval()
+    kc = torch.randn(1, 3, 7, 16)
+    with torch.no_grad(), pytest.raises((RuntimeError, ValueError)):
+        m(torch.randn(1, 2, 64), kv_cache=(kc, kc))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_paged_decode_layout_checks_precede_dtype_routes(dtype):
+    """Every pool dtype (the fp32 route included) checks the pools' contiguity, the
+    tables' dtype and their width against max_context_len before anything reads them;
+    on host tensors these raise before the device check."""
+    from fastest_flash_attention_amd.ops.kv_cache import fastest_flash_paged_decode
+
+    P, Hkv, D = 4, 2, 8
+    kp = torch.zeros(6, Hkv, P, D, dtype=dtype)
+    q = torch.zeros(2, 4, D, dtype=dtype)
+    lens = torch.tensor([9, 3], dtype=torch.int32)
+    narrow = torch.zeros(2, 2, dtype=torch.int32)  # 2 pages of 4 < 9 tokens
+    with pytest.raises(ValueError, match="fewer columns"):
+        fastest_flash_paged_decode(q, kp, kp, narrow, lens)
+    wide = torch.zeros(2, 3, dtype=torch.int32)
+    strided = torch.zeros(6, Hkv, P, 2 * D, dtype=dtype)[..., ::2]
+    with pytest.raises(ValueError, match="contiguous"):
+        fastest_flash_paged_decode(q, strided, strided, wide, lens)
+    with pytest.raises(TypeError, match="int32"):
+        fastest_flash_paged_decode(q, kp, kp, wide.long(), lens)
+    with pytest.raises(RuntimeError, match="ROCm"):  # valid layout: the device check
+        fastest_flash_paged_decode(q, kp, kp, wide, lens)

@@ -99,3 +99,43 @@ def test_noalloc_scratch_limit_is_checked_on_the_host():
     assert need > _lib.FFA_NOALLOC_SCRATCH_BYTES
     assert lib.ffa_paged_decode_fwd_noalloc(ctypes.byref(a), None) == -10
     assert b"static scratch" in lib.ffa_strerror(-10)
+
+
+@pytest.mark.gpu
+def test_noalloc_decode_graph_replays_match_eager():
+    """The allocation-free decode captured into a HIP graph (after one eager call on the
+    device, which resolves the scratch array's address) and replayed three times with q
+    refilled in place and eager work between replays: every replay equals the workspace
+    entry point on the same inputs bit for bit."""
+    require_gpu()
+    lib = _lib.load()
+    lens, Hq, Hkv, D, P, tps = [515, 17, 1030, 64], 8, 2, 128, 16, 128
+    q, kp, vp, bt, lens_t = _problem(7, lens, Hq, Hkv, D, P)
+    max_len = max(lens)
+    need = lib.ffa_paged_decode_workspace_bytes(len(lens), Hq, D, max_len, tps)
+    ws = torch.empty(max(need, 16), dtype=torch.uint8, device="cuda")
+    o_ref = torch.empty_like(q)
+    l_ref = torch.empty(len(lens), Hq, dtype=torch.float32, device="cuda")
+    o = torch.empty_like(q)
+    lse = torch.empty(len(lens), Hq, dtype=torch.float32, device="cuda")
+    a_ref = _args(q, kp, vp, bt, lens_t, o_ref, l_ref, max_len, tps, workspace=ws)
+    a = _args(q, kp, vp, bt, lens_t, o, lse, max_len, tps)
+    say("no-alloc decode: graph capture")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.ffa_paged_decode_fwd_noalloc(ctypes.byref(a), stream) == 0  # eager first
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        assert lib.ffa_paged_decode_fwd_noalloc(ctypes.byref(a), cap) == 0
+    for rep in range(3):
+        gen = torch.Generator().manual_seed(200 + rep)
+        q.copy_(torch.randn(q.shape, generator=gen).to(BF16))
+        o.fill_(float("nan"))
+        lse.fill_(float("nan"))
+        graph.replay()
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        assert lib.ffa_paged_decode_fwd(ctypes.byref(a_ref), stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref), f"replay {rep}: O differs"
+        assert torch.equal(lse, l_ref), f"replay {rep}: LSE differs"
