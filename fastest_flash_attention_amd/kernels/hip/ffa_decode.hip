@@ -1206,7 +1206,11 @@ namespace {
 template <typename Tag>
 void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3 grid,
                     hipStream_t s) {
-  const bool tile_page = mp.P % kMlaTile == 0;
+  // The whole-tile page path serves latent 512 only. Its latent-256 instantiation gave
+  // wrong scores on MI355X (deterministically, for some lanes of one key block: a K
+  // operand read returned the 16 bytes of a later k-step's read) although its LDS tile
+  // and Q registers were verified correct; the per-row page path computes latent 256.
+  const bool tile_page = mp.P % kMlaTile == 0 && dim_v == 512;
   if (dim_v == 512) {
     if (tile_page) {
       hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512, true>), grid, dim3(kMlaThreads), 0, s, mp);
@@ -1214,11 +1218,7 @@ void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3
       hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512, false>), grid, dim3(kMlaThreads), 0, s, mp);
     }
   } else {
-    if (tile_page) {
-      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256, true>), grid, dim3(kMlaThreads), 0, s, mp);
-    } else {
-      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256, false>), grid, dim3(kMlaThreads), 0, s, mp);
-    }
+    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256, false>), grid, dim3(kMlaThreads), 0, s, mp);
   }
   const unsigned heads4 = static_cast<unsigned>((static_cast<int64_t>(cp.B) * cp.Hq + 3) / 4);
   if (cp.n_splits <= 8) {
