@@ -295,20 +295,30 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   }
 
   // Q^T as the B operand: lane holds row qrow (clamped: rows past Sq are never
-  // stored), dims 16*ks + 8g .. +7.
-  // A negative scale is applied as q.k * scale = (-q).k * |scale|: the sign bits of Q
-  // are flipped here (exact), so the kernel's multiplier stays positive.
+  // stored), dims 16*ks + 8g .. +7. The loads are issued from inline asm ahead of the
+  // first tiles' global -> LDS loads, so that one memory round trip serves both: the
+  // compiler, which would wait for compiler-issued Q loads before issuing anything
+  // else, does not see them, and the prologue's wait for K(0) also covers Q (loads
+  // retire in issue order). On MI355X: -1 round trip of start-up per workgroup.
   u32x4 qreg[S::KS];
   {
     const uint16_t* qr = qbase + static_cast<int64_t>(min(qrow, p.Sq - 1)) * p.q_ss;
-    const uint32_t qx = p.q_neg ? 0x80008000u : 0u;
 #pragma unroll
     for (int ks = 0; ks < S::KS; ++ks) {
       const int d0 = min(16 * ks + 8 * g, D - 8);
-      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + d0) ^ qx;
-      qreg[ks] = (16 * ks + 8 * g < D) ? v : u32x4{0u, 0u, 0u, 0u};
+      asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(qreg[ks]) : "v"(qr + d0) : "memory");
     }
   }
+  // Once the loads are complete (wait_q below): a negative scale is applied as
+  // q.k * scale = (-q).k * |scale|, the sign bits of Q flipped (exact), so the kernel's
+  // multiplier stays positive; dims past head_dim are zero.
+  auto finish_q = [&]() __attribute__((always_inline)) {
+    const uint32_t qx = p.q_neg ? 0x80008000u : 0u;
+#pragma unroll
+    for (int ks = 0; ks < S::KS; ++ks) {
+      qreg[ks] = (16 * ks + 8 * g < D) ? (qreg[ks] ^ qx) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
 
   f32x16 oacc[SV::DB];
 #pragma unroll
@@ -551,6 +561,18 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
       }
       float pv[8];
       float csum = chunk_exp(nb, base, pv);
+      if constexpr (IL) {
+        // one S^T(t+1) MFMA, then four VALU instructions of the chunk's exponentials,
+        // and so on: on MI355X +1.6 % at the north-star shape, +3 % at S = 4096
+        // against the compiler's own order, bit-identical
+        if (do_qk) {
+#pragma unroll
+          for (int m = 0; m < S::KS * S::NB / S::NC; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+          }
+        }
+      }
       if (!checked && __any(!(csum <= lim))) {
         checked = true;
         const float mt = tile_max();
@@ -582,16 +604,26 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   if (n_it > 0) {
     issue_k(tile_at(0), k_lds[0]);
     issue_v(tile_at(0), v_lds[0]);
-    // S^T(0) needs K(0) only: the loads retire in issue order, so waiting until V(0)
-    // and K(1) alone may be outstanding (SV::LPT + S::LPT loads per thread; V tiles
-    // are narrower than K tiles in the narrow-V kernels) leaves K(0) complete, and
-    // their latency overlaps S^T(0) (the first step's wait and barrier cover them)
+    // S^T(0) needs Q and K(0) only: the loads retire in issue order, so waiting until
+    // V(0) and K(1) alone may be outstanding (SV::LPT + S::LPT loads per thread; V
+    // tiles are narrower than K tiles in the narrow-V kernels) leaves Q and K(0)
+    // complete, and their latency overlaps S^T(0) (the first step's wait and barrier
+    // cover them)
     if (n_it > 1) {
       issue_k(tile_at(1), k_lds[1]);
       wait_vmcnt<SV::LPT + S::LPT>();
     } else {
       wait_vmcnt<SV::LPT>();
     }
+  } else {
+    wait_vmcnt0();
+  }
+  // The Q registers hold the loaded values from here on (the asm below orders every
+  // use after the wait, and keeps the registers allocated to Q until then).
+#pragma unroll
+  for (int ks = 0; ks < S::KS; ++ks) asm volatile("" : "+v"(qreg[ks]) :: "memory");
+  finish_q();
+  if (n_it > 0) {
     __syncthreads();
     if (wave_live) qk(k_lds[0], s_cur);
   }
