@@ -90,9 +90,9 @@ struct BwdParams {
 
 // Workgroup -> (unit u = batch x head, tile j; j = 0 the heaviest causal tile): the
 // XCD-aware order of ffa_grid.h, the same as the forward kernel's grid, with the
-// group the launcher chose (bwd_xcd_group).
+// group the launcher chose (prefill_grid_order).
 __device__ inline void bwd_item(int bid, int n_t, int g, int remap, int& u, int& j) {
-  bwd_work_item(bid, static_cast<int>(gridDim.x), n_t, g, remap, u, j);
+  prefill_work_item(bid, static_cast<int>(gridDim.x), n_t, g, remap, u, j);
   u = __builtin_amdgcn_readfirstlane(u);
   j = __builtin_amdgcn_readfirstlane(j);
 }
@@ -1567,10 +1567,14 @@ int launch_attn_bwd(const ffa_attn_bwd_args& a, hipStream_t stream) {
     return FFA_ERR_TOO_LARGE;
   }
   if (grid_pre == 0 || grid_dq == 0) return FFA_OK;
-  p.xcd_remap_dq = bwd_xcd_remap(grid_dq);
-  p.xcd_remap_dkv = bwd_xcd_remap(grid_dkv);
-  p.xcd_group_dq = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_q, p.n_qt);
-  p.xcd_group_dkv = bwd_xcd_group(p.causal, static_cast<int64_t>(a.batch) * a.heads_kv, p.n_kt);
+  // the forward's grid order: each XCD runs its units one after another (their K / V,
+  // or Q / dO, stay in its L2) and interleaves only its last ones. At the north-star
+  // shape the step reads 0.53 GB less than with every pair interleaved (4.24 against
+  // 4.78 GB per backward); time within +-0.5 %, +5 % at head_dim 64.
+  prefill_grid_order(p.causal, static_cast<int64_t>(a.batch) * a.heads_q, grid_dq, p.xcd_group_dq,
+                     p.xcd_remap_dq);
+  prefill_grid_order(p.causal, static_cast<int64_t>(a.batch) * a.heads_kv, grid_dkv,
+                     p.xcd_group_dkv, p.xcd_remap_dkv);
   if (a.dtype == FFA_DTYPE_FP32) {
     // 32-row / 32-key workgroups
     const int64_t g32 = static_cast<int64_t>(a.batch) * a.heads_q * ((a.seqlen_q + 31) / 32) +

@@ -62,35 +62,7 @@ constexpr void prefill_grid_order(bool causal, int64_t n_units, int64_t grid, in
   xcd_group = (causal && n_units % 8 == 0) ? (n_units / 8 <= 8 ? 8 : (n_qt <= 32 ? 4 : 2)) : 0;
 }
 
-// Backward (dK/dV and dQ grids): grid = n_units * n_t, tile j = 0 the heaviest causal
-// tile. With group g > 0 (needs n_units % (8 g) == 0), XCD x owns units [x HX,
-// (x + 1) HX) and runs them g at a time, the g units' tiles interleaved heaviest first;
-// otherwise as the prefill map without a group.
-constexpr void bwd_work_item(int bid, int grid, int n_t, int g, int remap, int& unit, int& j) {
-  if (g > 0) {
-    const int hx = (grid / n_t) >> 3;
-    const int x = bid & 7;
-    const int k = bid >> 3;
-    const int gi = k / (g * n_t);
-    const int r = k - gi * g * n_t;
-    j = r / g;
-    unit = x * hx + gi * g + (r - j * g);
-    return;
-  }
-  if (remap) {
-    const int per_xcd = grid >> 3;
-    bid = (bid & 7) * per_xcd + (bid >> 3);
-  }
-  unit = bid / n_t;
-  j = bid - unit * n_t;
-}
-
-// The backward launcher's choice: causal grids whose units split evenly over the 8
-// XCDs in pairs, with a pair's tiles within 256 workgroups, run two units interleaved.
-constexpr int bwd_xcd_group(bool causal, int64_t n_units, int n_t) {
-  return (!causal || n_units % 16 != 0 || 2 * static_cast<int64_t>(n_t) > 256) ? 0 : 2;
-}
-
-constexpr int bwd_xcd_remap(int64_t grid) { return (grid % 8 == 0) ? 1 : 0; }
+// The backward's dK/dV and dQ grids (unit = batch x head, tile j = 0 the heaviest causal
+// tile) use the same map and the same launcher choice as the prefill.
 
 }  // namespace ffa

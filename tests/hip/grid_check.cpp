@@ -50,11 +50,14 @@ bool check_prefill(int n_units, int n_qt, bool causal) {
   });
 }
 
+// the backward grids: the prefill map, chosen per launch as the prefill's is, over the
+// dK/dV grid's (batch x kv-head, key tile) and the dQ grid's (batch x q-head, row tile)
 bool check_bwd(int n_units, int n_t, bool causal) {
-  const int group = ffa::bwd_xcd_group(causal, n_units, n_t);
-  const int remap = ffa::bwd_xcd_remap(static_cast<int64_t>(n_units) * n_t);
+  int group = 0;
+  int remap = 0;
+  ffa::prefill_grid_order(causal, n_units, static_cast<int64_t>(n_units) * n_t, group, remap);
   return check("backward", n_units, n_t, group, remap, [&](int bid, int grid, int& u, int& j) {
-    ffa::bwd_work_item(bid, grid, n_t, group, remap, u, j);
+    ffa::prefill_work_item(bid, grid, n_t, group, remap, u, j);
   });
 }
 

@@ -39,8 +39,8 @@ def test_grid_maps_are_bijections(tmp_path):
 @pytest.mark.parametrize("old,new", [
     # interleaved tail: tile index computed from the wrong group size
     ("jq = r / gl;", "jq = r / xcd_group;"),
-    # backward pairs: unit offset within the pair dropped
-    ("unit = x * hx + gi * g + (r - j * g);", "unit = x * hx + gi * g;"),
+    # units run in turn: unit index within the XCD dropped
+    ("      unit = x * hx + u;", "      unit = x * hx;"),
 ])
 def test_grid_check_catches_planted_mistakes(tmp_path, old, new):
     with open(os.path.join(HIP_DIR, "ffa_grid.h")) as f:
