@@ -331,7 +331,15 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   float negmc = 0.0f;   // -m_run * c (0 while m_run = -inf)
   float lim = -1.0f;    // chunk exp-sum limit; < 0: no max yet, the first chunk sets it
 
-  auto qk = [&](const uint16_t* kl, f32x16 (&sacc)[S::NB]) __attribute__((always_inline)) {
+  // S^T of one tile. FENCE keeps each k-step's MFMAs behind a scheduling barrier (the
+  // K operand reads stay one k-step ahead). Without it (the fast step at head_dim >= 192,
+  // where S^T(t+1) is a block of 24-32 MFMAs ahead of softmax(t)) the compiler spreads
+  // the tile's max and softcap VALU work of tile t between those MFMAs: +2 % at the MLA
+  // prefill shape, +5-6 % at head_dim 192 with softcap and at 256 on MI355X,
+  // bit-identical (two head_dim-192 kernels then use 12 B per lane of scratch, reloaded in
+  // the general-step loops, not in the fast loop; still faster).
+  auto qk = [&](const uint16_t* kl, f32x16 (&sacc)[S::NB], auto fence) __attribute__((always_inline)) {
+    constexpr bool FENCE = decltype(fence)::value;
 #pragma unroll
     for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll
@@ -373,7 +381,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
           a_nxt[nb] = *reinterpret_cast<const u32x4*>(kl + k_rd(ks + 1) + nb * 32 * DP);
         }
       }
-      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (FENCE) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int nb = 0; nb < S::NB; ++nb) sacc[nb] = E::mfma32(a_cur[nb], qreg[ks], sacc[nb]);
 #pragma unroll
@@ -625,7 +633,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   finish_q();
   if (n_it > 0) {
     __syncthreads();
-    if (wave_live) qk(k_lds[0], s_cur);
+    if (wave_live) qk(k_lds[0], s_cur, std::true_type{});
   }
   // Iteration i computes tile t = t_begin + i. Entering it, K(t+1) and V(t) are in
   // LDS; it issues K(t+2) and V(t+1) into the buffers iteration i-1 finished reading,
@@ -639,7 +647,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     if (i + 1 < n_it) issue_v(tile_at(i + 1), v_lds[(i + 1) & 1]);
     if (!wave_live) return;
     if (p.causal && t * BN > qwl_abs) return;  // past this wave's causal band
-    if (!IL && i + 1 < n_it) qk(k_lds[(i + 1) & 1], nxt);
+    if (!IL && i + 1 < n_it) qk(k_lds[(i + 1) & 1], nxt, std::true_type{});
     softmax_pv(cur, t, v_lds[i & 1], std::true_type{}, kmask_partial(i), nxt, k_lds[(i + 1) & 1],
                i + 1 < n_it, [](int) {});
   };
@@ -655,7 +663,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     if (!IL) {
       issue_full(S{}, k_next, k_tile_bytes, k_off, k_wlds, std::integral_constant<uint32_t, PAR>{});
       issue_full(SV{}, v_next, v_tile_bytes, v_off, v_wlds, std::integral_constant<uint32_t, 1 - PAR>{});
-      qk(k_lds[1 - PAR], nxt);
+      qk(k_lds[1 - PAR], nxt, std::integral_constant<bool, (DP < 192)>{});
       softmax_pv(cur, t, v_lds[PAR], std::false_type{}, false, nxt, k_lds[1 - PAR], true, [](int) {});
     } else {
       // The tile loads spread over the P V chunks (chunk cc issues loads

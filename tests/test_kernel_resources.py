@@ -25,6 +25,12 @@ EXCEPTIONS = {
     # narrow-V head_dim 192 with softcap: 64-key tiles at 256 VGPRs (still faster than
     # 32-key tiles without spills, 0.391 vs 0.401 ms at the MLA prefill shape)
     r"prefill_kernel<.*, 192, 128, 64, true>": 16,
+    # head_dim 192 fast step with the softmax's max spread between the S^T MFMAs (no
+    # scheduling fence): 12 B reloaded in the general-step loops (not the fast loop),
+    # 2-6 % faster than the fenced, spill-free form (the MLA prefill shape; head_dim 192
+    # with softcap)
+    r"prefill_kernel<.*, 192, 128, 64, false>": 12,
+    r"prefill_kernel<.*, 192, 192, 32, true>": 12,
 }
 
 
