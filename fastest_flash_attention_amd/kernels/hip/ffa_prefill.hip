@@ -53,23 +53,23 @@ constexpr int kMaxLiveTiles = 2048;
 // 0.351 ms with 32-key tiles and 0.397 ms for the zero-padded V on the 192-dim kernel.
 constexpr int kNarrowBN = 64;
 constexpr int kTileFull = 0x8000;  // list entry flag: the block mask keeps the whole tile
-constexpr size_t kLiveLdsBytes = 4 * sizeof(int) + kMaxLiveTiles * sizeof(uint16_t);
+constexpr size_t kLiveLdsBytes = 8 * sizeof(int) + kMaxLiveTiles * sizeof(uint16_t);
 // Workgroup -> (batch x head, query tile j; j = 0 is the heaviest causal tile): the
 // XCD-aware order of ffa_grid.h, with the group / remap the launcher chose.
 __device__ inline void work_item(const PrefillParams& p, int bid, int& bh, int& jq) {
   prefill_work_item(bid, static_cast<int>(gridDim.x), p.n_qt, p.xcd_group, p.xcd_remap, bh, jq);
 }
 
-template <int DP, int BN>
+template <int DP, int BN, int NW = 4>
 struct Shape {
   static constexpr int CPR = DP / 8;            // 16-byte chunks per row
   static constexpr int TILE = BN * DP;          // elements per K (or V) tile
-  static constexpr int LPT = BN * CPR / kThreads;  // direct loads per thread per tile
+  static constexpr int LPT = BN * CPR / (64 * NW);  // direct loads per thread per tile
   static constexpr int NB = BN / 32;
   static constexpr int NC = BN / 16;
   static constexpr int KS = DP / 16;
   static constexpr int DB = DP / 32;
-  static_assert(BN * CPR % kThreads == 0, "tile must split evenly over the workgroup");
+  static_assert(BN * CPR % (64 * NW) == 0, "tile must split evenly over the workgroup");
 };
 
 // Two workgroups per CU (2 waves per SIMD, <= 256 VGPRs) up to head_dim 192; the
@@ -83,18 +83,26 @@ constexpr int kMinBlocks = (DP == 64 && !SOFTCAP) ? 3 : (DP <= 192 ? 2 : 1);
 // DV: the V tile / O accumulator width (<= DP). It is DP except for head_dim 192 over
 // a V of at most 128 dims (the MLA prefill's V, which its caller would otherwise
 // zero-pad to 192): P V then runs over the 128 real dims only.
-template <typename Tag, int DP, int DV, int BN, bool SOFTCAP>
-__global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_kernel(const PrefillParams p) {
-  using S = Shape<DP, BN>;   // Q, K tiles, S^T
-  using SV = Shape<DV, BN>;  // V tiles, O^T
+// NW: waves per workgroup, each owning 32 query rows (a workgroup covers 32 NW rows).
+// Four, two workgroups per CU, except the narrow-V kernels on long sequences: eight
+// waves, one workgroup per CU, so each K/V tile is loaded once for 256 rows (half the
+// tile loads per FLOP of two 4-wave workgroups). On MI355X at the MLA prefill shape
+// (B 2, H 32, S 4096): +4-6 % causal, +5 % non-causal, +-0-2 % with softcap, outputs
+// bit-identical, and the kernel stops spilling; the head_dim-128 kernels lose 3-8 %
+// with eight waves, and shorter causal sequences lose too (-10 % at S = 2048).
+template <typename Tag, int DP, int DV, int BN, bool SOFTCAP, int NW>
+__global__ __launch_bounds__((64 * NW), (kMinBlocks<DP, SOFTCAP> * 4 / NW)) void prefill_kernel(const PrefillParams p) {
+  constexpr int BM = 32 * NW;  // query rows per workgroup
+  using S = Shape<DP, BN, NW>;   // Q, K tiles, S^T
+  using SV = Shape<DV, BN, NW>;  // V tiles, O^T
   using E = Elem<Tag>;
   __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][S::TILE];
   __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][SV::TILE];
   // Block mask: the tiles to visit, in dynamic LDS that only launches with a block mask
   // request (kLiveLdsBytes), so that the K/V buffers alone set the occupancy otherwise.
   extern __shared__ __attribute__((aligned(16))) int live_dyn[];
-  int* const live_cnt = live_dyn;                                       // [4]
-  uint16_t* const live_lds = reinterpret_cast<uint16_t*>(live_dyn + 4);  // [kMaxLiveTiles]
+  int* const live_cnt = live_dyn;                                       // [NW <= 8]
+  uint16_t* const live_lds = reinterpret_cast<uint16_t*>(live_dyn + 8);  // [kMaxLiveTiles]
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -117,8 +125,8 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   const int D = p.D;
   const int Skv = p.Skv;
 
-  const int q0 = qt * kBlockM;
-  const int q_last = min(q0 + kBlockM, p.Sq) - 1;
+  const int q0 = qt * BM;
+  const int q_last = min(q0 + BM, p.Sq) - 1;
   const int q0_abs = p.q_offset + q0;
   const int ql_abs = p.q_offset + q_last;
   const int kv_lo = p.window > 0 ? max(0, q0_abs - p.window + 1) : 0;
@@ -148,7 +156,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     const int rb0 = q0 / p.ref_bq;
     const int rb1 = q_last / p.ref_bq;
     int n_live = 0;
-    for (int base = 0; base < nt; base += kThreads) {
+    for (int base = 0; base < nt; base += 64 * NW) {
       const int i = base + tid;
       bool live = false;
       bool full = true;  // every key of the tile set for every row: no element mask
@@ -171,7 +179,8 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
         live_lds[off + __popcll(bal & ((uint64_t{1} << lane) - 1))] =
             static_cast<uint16_t>(i | (full ? kTileFull : 0));
       }
-      n_live += live_cnt[0] + live_cnt[1] + live_cnt[2] + live_cnt[3];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) n_live += live_cnt[w];
       __syncthreads();
     }
     n_it = n_live;
@@ -200,7 +209,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   uint32_t k_off[S::LPT], v_off[SV::LPT];
 #pragma unroll
   for (int j = 0; j < S::LPT; ++j) {
-    const int pos = (4 * j + wave) * 64 + lane;
+    const int pos = (NW * j + wave) * 64 + lane;
     const int row = pos / S::CPR;
     const int q = pos - row * S::CPR;
     const int kc = min(q ^ kswz<DP>(row), dchunks - 1);
@@ -208,7 +217,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   }
 #pragma unroll
   for (int j = 0; j < SV::LPT; ++j) {
-    const int pos = (4 * j + wave) * 64 + lane;
+    const int pos = (NW * j + wave) * 64 + lane;
     const int row = pos / SV::CPR;
     const int q = pos - row * SV::CPR;
     const int vc = min(q ^ vswz<DV>(row), dvchunks - 1);
@@ -228,23 +237,23 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     if (t < t_full) {
 #pragma unroll
       for (int j = 0; j < SH::LPT; ++j) {
-        load_lds16_async(tb, off[j], lds_addr(dst + (4 * j + wave) * 512));
+        load_lds16_async(tb, off[j], lds_addr(dst + (NW * j + wave) * 512));
       }
     } else {
       // last tile: rows past Skv re-read row Skv-1 (their scores are masked to -inf)
       const int kt0 = t * BN;
 #pragma unroll
       for (int j = 0; j < SH::LPT; ++j) {
-        const int row = ((4 * j + wave) * 64 + lane) / SH::CPR;
+        const int row = ((NW * j + wave) * 64 + lane) / SH::CPR;
         const int over = max(0, kt0 + row - (Skv - 1));
         const uint32_t back = static_cast<uint32_t>(over * stride * 2);
-        load_lds16_async(tb, off[j] - back, lds_addr(dst + (4 * j + wave) * 512));
+        load_lds16_async(tb, off[j] - back, lds_addr(dst + (NW * j + wave) * 512));
       }
     }
     tb += tile_bytes;
   };
   // LDS byte address of this wave's first load slot in buffer 0 of K and of V (uniform,
-  // SGPRs): load j of buffer b writes at base + b * TILE * 2 + j * 4 KiB.
+  // SGPRs): load j of buffer b writes at base + b * TILE * 2 + j * NW KiB.
   const uint32_t k_wlds = __builtin_amdgcn_readfirstlane(lds_addr(&k_lds[0][0]) + wave * 1024);
   const uint32_t v_wlds = __builtin_amdgcn_readfirstlane(lds_addr(&v_lds[0][0]) + wave * 1024);
   // A tile known to hold BN keys (no tail handling, no test) into buffer B.
@@ -254,7 +263,7 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
     constexpr uint32_t B = decltype(buf)::value;
 #pragma unroll
     for (int j = 0; j < SH::LPT; ++j) {
-      load_lds16_async(tb, off[j], wlds + B * SH::TILE * 2 + j * 4096);
+      load_lds16_async(tb, off[j], wlds + B * SH::TILE * 2 + j * 1024 * NW);
     }
     tb += tile_bytes;
   };
@@ -674,11 +683,11 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
                  [&](int cc) __attribute__((always_inline)) {
 #pragma unroll
                    for (int j = S::LPT * cc / S::NC; j < S::LPT * (cc + 1) / S::NC; ++j) {
-                     load_lds16_async(k_next, k_off[j], k_wlds + PAR * S::TILE * 2 + j * 4096);
+                     load_lds16_async(k_next, k_off[j], k_wlds + PAR * S::TILE * 2 + j * 1024 * NW);
                    }
 #pragma unroll
                    for (int j = SV::LPT * cc / S::NC; j < SV::LPT * (cc + 1) / S::NC; ++j) {
-                     load_lds16_async(v_next, v_off[j], v_wlds + (1 - PAR) * SV::TILE * 2 + j * 4096);
+                     load_lds16_async(v_next, v_off[j], v_wlds + (1 - PAR) * SV::TILE * 2 + j * 1024 * NW);
                    }
                  });
       k_next += k_tile_bytes;
@@ -743,14 +752,36 @@ __global__ __launch_bounds__(kThreads, (kMinBlocks<DP, SOFTCAP>)) void prefill_k
   }
 }
 
-template <typename Tag, int DP, int DV, int BN>
-void launch_dp(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
+template <typename Tag, int DP, int DV, int BN, int NW>
+void launch_nw(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
   const size_t dyn = p.kmask != nullptr ? kLiveLdsBytes : 0;
   if (softcap) {
-    hipLaunchKernelGGL((prefill_kernel<Tag, DP, DV, BN, true>), dim3(grid), dim3(kThreads), dyn, s, p);
+    hipLaunchKernelGGL((prefill_kernel<Tag, DP, DV, BN, true, NW>), dim3(grid), dim3(64 * NW), dyn, s, p);
   } else {
-    hipLaunchKernelGGL((prefill_kernel<Tag, DP, DV, BN, false>), dim3(grid), dim3(kThreads), dyn, s, p);
+    hipLaunchKernelGGL((prefill_kernel<Tag, DP, DV, BN, false, NW>), dim3(grid), dim3(64 * NW), dyn, s, p);
   }
+}
+
+template <typename Tag, int DP, int DV, int BN>
+void launch_dp(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
+  launch_nw<Tag, DP, DV, BN, 4>(p, softcap, grid, s);
+}
+
+// The narrow-V kernels run eight waves (256-row workgroups) from kWideRowsFrom query
+// rows on: the query tiles, the grid and its XCD order are re-derived for 256 rows.
+constexpr int kWideRowsFrom = 4096;
+
+template <typename Tag>
+void launch_narrow(const PrefillParams& p0, bool softcap, int grid, hipStream_t s) {
+  if (p0.Sq < kWideRowsFrom) {
+    launch_nw<Tag, 192, 128, kNarrowBN, 4>(p0, softcap, grid, s);
+    return;
+  }
+  PrefillParams p = p0;
+  p.n_qt = (p.Sq + 255) / 256;
+  const int grid8 = p.n_qt * p.B * p.Hq;
+  prefill_grid_order(p.causal != 0, static_cast<int64_t>(p.B) * p.Hq, grid8, p.xcd_group, p.xcd_remap);
+  launch_nw<Tag, 192, 128, kNarrowBN, 8>(p, softcap, grid8, s);
 }
 
 template <typename Tag>
@@ -763,7 +794,7 @@ void launch_tag(const PrefillParams& p, bool softcap, int grid, hipStream_t s) {
     launch_dp<Tag, 128, 128, 64>(p, softcap, grid, s);
   } else if (p.D <= 192) {
     if (p.Dv <= 128) {
-      launch_dp<Tag, 192, 128, kNarrowBN>(p, softcap, grid, s);
+      launch_narrow<Tag>(p, softcap, grid, s);
     } else {
       launch_dp<Tag, 192, 192, 32>(p, softcap, grid, s);
     }

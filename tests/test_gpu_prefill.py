@@ -73,6 +73,10 @@ NARROW_V = [
     ("d136_dv64_fp16", 1, 2, 2, 100, 100, 136, 64, {"causal": True}, F16),
     ("d160_dv120_window", 1, 2, 2, 260, 260, 160, 120, {"sliding_window": 50}, BF16),
     ("mla_negative_scale", 1, 2, 2, 140, 140, 192, 128, {"causal": True, "scale": -0.1}, BF16),
+    # from 4096 query rows on the narrow-V kernels run 256-row (eight-wave) workgroups
+    ("mla_wide_causal_ragged", 1, 1, 1, 4100, 4100, 192, 128, {"causal": True}, BF16),
+    ("mla_wide_gqa_window_softcap", 1, 2, 1, 4096, 4400, 192, 128,
+     {"sliding_window": 700, "softcap": 30.0, "num_kv_heads": 1}, BF16),
     ("host_padded_d128_dv64", 1, 2, 2, 90, 90, 128, 64, {"causal": True}, BF16),
     ("host_padded_dv100", 1, 2, 2, 90, 90, 192, 100, {"causal": True}, BF16),
 ]
