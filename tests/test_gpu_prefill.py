@@ -77,6 +77,7 @@ NARROW_V = [
     ("mla_wide_causal_ragged", 1, 1, 1, 4100, 4100, 192, 128, {"causal": True}, BF16),
     ("mla_wide_gqa_window_softcap", 1, 2, 1, 4096, 4400, 192, 128,
      {"sliding_window": 700, "softcap": 30.0, "num_kv_heads": 1}, BF16),
+    ("wide_d160_dv120_fp16", 1, 1, 1, 4096, 4096, 160, 120, {"causal": True}, F16),
     ("host_padded_d128_dv64", 1, 2, 2, 90, 90, 128, 64, {"causal": True}, BF16),
     ("host_padded_dv100", 1, 2, 2, 90, 90, 192, 100, {"causal": True}, BF16),
 ]
