@@ -458,16 +458,29 @@ __global__ __launch_bounds__((64 * NW), (kMinBlocks<DP, SOFTCAP> * 4 / NW)) void
     // the tile's row max in score units (softcap: 1 - 2 min r)
     auto tile_max = [&]() __attribute__((always_inline)) {
       if constexpr (LATE_CAP) {
-        // raw scores: tanh is increasing, so the transformed max is the transform of
-        // the raw max (r = 1 / (1 + e^{2y}) is decreasing)
-        float mr = kNegInf;
+        // raw scores: r = 1 / (1 + 2^x) decreases in x = s * tanh_mul, so the tile's
+        // smallest r (largest tanh) is the transform of the largest x: of the largest s,
+        // or of the smallest for a negative multiplier (a negative scale). Both are taken
+        // on s itself (max of s or of -s), so no product s * tanh_mul is formed here for
+        // the compiler to keep live for the chunks' own transform.
+        const bool up = tanh_mul >= 0.0f;  // uniform
+        float mx = kNegInf;
+        if (up) {
 #pragma unroll
-        for (int nb2 = 0; nb2 < S::NB; ++nb2) {
+          for (int nb2 = 0; nb2 < S::NB; ++nb2) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mr = fmaxf(mr, sacc[nb2][r]);
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[nb2][r]);
+          }
+        } else {
+#pragma unroll
+          for (int nb2 = 0; nb2 < S::NB; ++nb2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, -sacc[nb2][r]);
+          }
         }
-        mr = wave_pair_max(mr);
-        return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + fast_exp2(mr * tanh_mul)), 1.0f);
+        mx = wave_pair_max(mx);
+        const float x = (up ? mx : -mx) * tanh_mul;
+        return fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + fast_exp2(x)), 1.0f);
       }
       float mt = SOFTCAP ? __builtin_inff() : kNegInf;
 #pragma unroll

@@ -42,6 +42,16 @@ SCALES = [
     ("zero_fp32", torch.float32, 0.0, None, False),
     ("neg_fp32_softcap", torch.float32, -0.25, 6.0, True),
 ]
+# Longer sweeps whose interior tiles run the kernels' fast step (its softcap transform
+# and running max are its own code): a negative scale with a large cap and scores that
+# span most of tanh's range, where a max taken in the wrong direction overflows the
+# exponentials (cap * log2(e) * 2 > 128).
+SCALES_LONG = [
+    ("neg_softcap_long_d128", BF16, -3.0, 50.0, False, 128),
+    ("neg_softcap_long_d64", BF16, -3.0, 50.0, True, 64),
+    ("pos_softcap_long_d128", BF16, 3.0, 50.0, True, 128),
+    ("neg_softcap_narrow_range", BF16, -0.3, 50.0, False, 128),
+]
 
 
 @pytest.mark.parametrize("name,dtype,scale,softcap,causal", SCALES, ids=[s[0] for s in SCALES])
@@ -66,6 +76,22 @@ def test_abi_scale_contract(name, dtype, scale, softcap, causal):
         # uniform softmax over the visible keys: lse = log(n)
         n = np.arange(1, S + 1) if causal else np.full(S, S)
         assert np.allclose(np32(call.lse)[0, :, :, 0], np.log(n)[None, :], atol=1e-5)
+
+
+@pytest.mark.parametrize("name,dtype,scale,softcap,causal,D", SCALES_LONG,
+                         ids=[s[0] for s in SCALES_LONG])
+def test_scale_softcap_fast_step(name, dtype, scale, softcap, causal, D):
+    require_gpu()
+    B, H, S = 1, 2, 1024
+    q, k, v = (seeded((B, H, S, D), dtype, s) for s in (41, 42, 43))
+    say(f"scale {name} {dtype} scale={scale} softcap={softcap} causal={causal} D{D}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), scale=scale,
+                                            causal=causal, softcap=softcap, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all() and torch.isfinite(lse).all()
+    ro, rl = rf.forward(np32(q), np32(k), np32(v), scale=scale, causal=causal, softcap=softcap,
+                        return_lse=True)
+    assert_parity(o, ro, lse, rl, name)
 
 
 def _masked_oracle(q, k_pages, v_pages, bt, lens, num_pages, scale):
