@@ -767,7 +767,9 @@ __global__ __launch_bounds__((64 * NW), (kMinBlocks<DP, SOFTCAP> * 4 / NW)) void
 
   const float l_tot = wave_pair_sum(l_run);
   if (wave_live && qrow < p.Sq) {
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    float lse = l_tot > 0.0f ? (m_run * c + fast_log2(l_tot)) * kLn2 : masked_row_lse(p, qrow);
+    if (l_tot > 0.0f) ref_tile_floor(p, qrow, lse, inv);
     uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;
     const int Dv = NARROW ? p.Dv : D;
 #pragma unroll
@@ -785,8 +787,6 @@ __global__ __launch_bounds__((64 * NW), (kMinBlocks<DP, SOFTCAP> * 4 / NW)) void
       for (int d0 = Dv + 4 * g; d0 < D; d0 += 8) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{0u, 0u};
     }
     if (p.lse != nullptr && g == 0) {
-      const float lse = l_tot > 0.0f ? (m_run * c + fast_log2(l_tot)) * kLn2
-                                     : masked_row_lse(p, qrow);
       p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(qrow) * p.l_ss] = lse;
     }
   }
@@ -1010,7 +1010,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillP
 
   const float l_tot = wave_pair_sum(l_run);
   if (wave_live && qrow < p.Sq) {
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    float lse = l_tot > 0.0f ? (m_run * c + fast_log2(l_tot)) * kLn2 : masked_row_lse(p, qrow);
+    if (l_tot > 0.0f) ref_tile_floor(p, qrow, lse, inv);
     float* orow = of + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -1023,8 +1025,6 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_f32_kernel(const PrefillP
       }
     }
     if (p.lse != nullptr && g == 0) {
-      const float lse = l_tot > 0.0f ? (m_run * c + fast_log2(l_tot)) * kLn2
-                                     : masked_row_lse(p, qrow);
       p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(qrow) * p.l_ss] = lse;
     }
   }
@@ -1231,7 +1231,9 @@ __global__ __launch_bounds__(kThreads, kF32SplitBlocks<DP>) void prefill_f32_spl
       oacc[db][r] = o;
     }
   }
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  float lse = l_tot > 0.0f ? (m * c + fast_log2(l_tot)) * kLn2 : masked_row_lse(p, qrow);
+  if (l_tot > 0.0f) ref_tile_floor(p, qrow, lse, inv);
   float* orow = of + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
@@ -1244,7 +1246,6 @@ __global__ __launch_bounds__(kThreads, kF32SplitBlocks<DP>) void prefill_f32_spl
     }
   }
   if (p.lse != nullptr && g == 0) {
-    const float lse = l_tot > 0.0f ? (m * c + fast_log2(l_tot)) * kLn2 : masked_row_lse(p, qrow);
     p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(qrow) * p.l_ss] = lse;
   }
 }

@@ -1,5 +1,6 @@
 // Pieces of the gfx950 prefill kernels (ffa_prefill.hip): the launch parameter block, the LDS row swizzles of K/V tiles and the reference's
-// LSE for rows that see no key.
+// per-tile 1e-30 floor of the softmax sum (the LSE of rows that see no key, and its
+// share in rows that do).
 #pragma once
 
 #include "ffa_common.h"
@@ -56,16 +57,11 @@ __device__ inline int vswz(int r) {
   return 4 * (r & 3);
 }
 
-// LSE of a row with no visible key, as the reference loop produces it: each visited
-// tile adds log(1e-30) by logaddexp (cpu_reference.py:288-297), so n visited tiles
-// give log(n) + log(1e-30); no visited tile leaves -inf. Tiles are the reference's
-// (ref_bq x ref_bkv) tiles, visited per cpu_reference.py:215-231.
-__device__ inline float masked_row_lse(const PrefillParams& p, int row) {
-  if (p.masked_lse_mode != 0) return kNegInf;
-  if (p.kmask != nullptr) {
-    const int n = p.visited[row / p.ref_bq];
-    return n > 0 ? logf(static_cast<float>(n)) + logf(1e-30f) : kNegInf;
-  }
+// The reference tiles (ref_bq x ref_bkv) that the reference loop visits for `row`'s row
+// block (cpu_reference.py:215-231): the block mask's count per row block, or the
+// causal / window range.
+__device__ inline int ref_visited_tiles(const PrefillParams& p, int row) {
+  if (p.kmask != nullptr) return p.visited[row / p.ref_bq];
   const int bq = p.ref_bq;
   const int bkv = p.ref_bkv;
   const int iq = row / bq;
@@ -84,9 +80,52 @@ __device__ inline float masked_row_lse(const PrefillParams& p, int row) {
     if (j >= n_bc - 1) j = (p.Skv - 1 >= thr) ? n_bc - 1 : n_bc;
     j_lo = j;
   }
-  const int n = j_hi - j_lo + 1;
-  if (n <= 0) return kNegInf;
-  return logf(static_cast<float>(n)) + logf(1e-30f);
+  return max(j_hi - j_lo + 1, 0);
+}
+
+// LSE of a row with no visible key, as the reference loop produces it: each visited
+// tile floors its row sum at 1e-30 and adds it by logaddexp (cpu_reference.py:288-297),
+// so n visited tiles give log(n) + log(1e-30); no visited tile leaves -inf.
+__device__ inline float masked_row_lse(const PrefillParams& p, int row) {
+  if (p.masked_lse_mode != 0) return kNegInf;
+  const int n = ref_visited_tiles(p, row);
+  return n > 0 ? logf(static_cast<float>(n)) + logf(1e-30f) : kNegInf;
+}
+
+// The same floor for a row that does see keys: every visited reference tile in which
+// the row sees none adds 1e-30 to its softmax sum. The kernels add it at the end:
+// lse becomes logaddexp(lse, log(k 1e-30)) and O is scaled by exp(lse_old - lse_new).
+// It only shows where the row's own sum is below about k 1e-30 (every visible logit
+// under about -69 + log k); elsewhere the correction is below fp32 resolution and is
+// skipped without counting the tiles. Not with the two-pass LSE (masked_lse_mode),
+// which the reference takes exactly.
+__device__ inline void ref_tile_floor(const PrefillParams& p, int row, float& lse, float& inv) {
+  // n < 2^31 tiles: log(n 1e-30) - lse <= -40 whenever lse > -8
+  if (p.masked_lse_mode != 0 || lse > -8.0f) return;
+  const int n = ref_visited_tiles(p, row);
+  if (n <= 0 || logf(static_cast<float>(n)) + logf(1e-30f) - lse <= -40.0f) return;
+  // visited tiles that hold a key this row sees: they all lie in [lo, hi] / ref_bkv
+  const int qa = p.q_offset + row;
+  const int lo = p.window > 0 ? max(0, qa - p.window + 1) : 0;
+  const int hi = p.causal ? min(qa, p.Skv - 1) : p.Skv - 1;
+  if (lo > hi) return;  // no visible key: the masked-row path
+  const int bkv = p.ref_bkv;
+  int seen = 0;
+  if (p.kmask != nullptr) {
+    // the key mask holds the block mask's bit at every key of a tile
+    const uint64_t* mrow = p.kmask + static_cast<int64_t>(row / p.ref_bq) * p.kmask_words;
+    for (int j = lo / bkv; j <= hi / bkv; ++j) {
+      const int key = j * bkv;
+      seen += static_cast<int>((mrow[key >> 6] >> (key & 63)) & 1u);
+    }
+  } else {
+    seen = hi / bkv - lo / bkv + 1;
+  }
+  const int k = n - seen;
+  if (k <= 0) return;
+  const float e = expf(logf(static_cast<float>(k)) + logf(1e-30f) - lse);
+  inv *= 1.0f / (1.0f + e);
+  lse += log1pf(e);
 }
 
 }  // namespace pf

@@ -78,6 +78,52 @@ def test_forward_sweep(case):
         assert max_abs < 1e-4, f"{name}: fp32 max-abs {max_abs:.2e}"
 
 
+def _draw_long(n: int, seed: int):
+    """Sweeps long enough that interior tiles run the kernels' fast step (its own max,
+    rescale and softcap code), with scales whose scores span a wide range: the running
+    max moves often and, with softcap, tanh spans most of [-1, 1]."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D, Dv = [(64, 64), (128, 128), (192, 128), (192, 192), (256, 256)][int(rng.integers(5))]
+        dt = (torch.bfloat16, torch.float16)[int(rng.integers(2))]
+        Hkv = int(rng.choice((1, 2)))
+        Hq = Hkv * int(rng.choice((1, 2)))
+        Sq = int(rng.integers(600, 1300))
+        Skv = Sq if rng.random() < 0.6 else int(rng.integers(600, 1300))
+        causal = bool(rng.random() < 0.5)
+        window = int(rng.integers(200, 700)) if rng.random() < 0.3 else None
+        softcap = float(rng.choice((20.0, 50.0))) if rng.random() < 0.5 else None
+        scale = float(rng.choice((-3.0, -0.5, 0.05, 0.5, 3.0)))
+        name = (f"{i}_H{Hq}-{Hkv}_S{Sq}x{Skv}_D{D}v{Dv}_{str(dt)[6:]}_c{int(causal)}_w{window}"
+                f"_cap{softcap}_s{scale}")
+        cases.append((name, Hq, Hkv, Sq, Skv, D, Dv, dt, causal, window, softcap, scale))
+    return cases
+
+
+LONG_CASES = _draw_long(16, 20261205)
+
+
+@pytest.mark.parametrize("case", LONG_CASES, ids=[c[0] for c in LONG_CASES])
+def test_forward_sweep_long_wide_range(case):
+    require_gpu()
+    name, Hq, Hkv, Sq, Skv, D, Dv, dt, causal, window, softcap, scale = case
+    seed = 11 + 17 * int(name.split("_")[0])
+    q = seeded((1, Hq, Sq, D), dt, seed)
+    k = seeded((1, Hkv, Skv, D), dt, seed + 1)
+    v = seeded((1, Hkv, Skv, Dv), dt, seed + 2)
+    kw = dict(causal=causal, sliding_window=window, softcap=softcap, scale=scale, return_lse=True)
+    if Hq != Hkv:
+        kw["num_kv_heads"] = Hkv
+    say(f"forward sweep long {name}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all(), f"{name}: non-finite output"
+    vp = torch.nn.functional.pad(v, (0, D - Dv))
+    ro, rl = rf.forward(np32(q), np32(k), np32(vp), **kw)
+    assert_parity(o, ro, lse, rl, name)
+
+
 @pytest.mark.parametrize("case", BWD_CASES, ids=[c[0] for c in BWD_CASES])
 def test_backward_sweep(case):
     require_gpu()

@@ -31,6 +31,9 @@ EXCEPTIONS = {
     # with softcap)
     r"prefill_kernel<.*, 192, 128, 64, false, 4>": 12,
     r"prefill_kernel<.*, 192, 192, 32, true, 4>": 12,
+    # the eight-wave narrow-V kernel with softcap: 16 B reloaded in the first general-step
+    # loop only (the epilogue's reference tile floor lengthens a few live ranges)
+    r"prefill_kernel<.*, 192, 128, 64, true, 8>": 16,
 }
 
 
