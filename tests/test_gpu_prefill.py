@@ -100,6 +100,38 @@ def test_prefill_narrow_v(case):
     assert_parity(o, ro, lse, rl, name)
 
 
+@pytest.mark.parametrize("dtype,D,block_mask", [(BF16, 64, False), (BF16, 192, False),
+                                               (torch.float32, 64, False), (BF16, 128, True)])
+def test_reference_tile_floor(dtype, D, block_mask):
+    """Every visited reference tile in which a row sees no key adds 1e-30 to that row's
+    softmax sum (the reference's clamp(min=1e-30) per tile). With every logit near -100
+    that floor, not the row's own keys, sets O and the LSE of most rows: the kernels must
+    add it for rows that see keys too, not only for fully masked rows."""
+    require_gpu()
+    B, H, S, bs = 1, 2, 300, 32
+    u = seeded((1, 1, 1, D), torch.float32, 61)
+    u = u / u.norm()
+    q = (-10.0 * u).expand(B, H, S, D) + 0.01 * seeded((B, H, S, D), torch.float32, 62)
+    k = (10.0 * u).expand(B, H, S, D) + 0.01 * seeded((B, H, S, D), torch.float32, 63)
+    q, k = q.to(dtype), k.to(dtype)
+    v = seeded((B, H, S, D), dtype, 64)
+    kw = dict(causal=True, sliding_window=40, scale=1.0, block_size=bs, return_lse=True)
+    if block_mask:
+        g = torch.Generator().manual_seed(65)
+        bm = torch.rand(math.ceil(S / bs), math.ceil(S / bs), generator=g) < 0.7
+        kw["block_mask"] = bm
+    say(f"reference tile floor {dtype} D{D} block_mask={block_mask}")
+    o, lse = ffa.fastest_flash_attn_forward(q.cuda(), k.cuda(), v.cuda(), **kw)
+    torch.cuda.synchronize()
+    okw = dict(kw)
+    if block_mask:
+        okw["block_mask"] = kw["block_mask"].numpy()
+    ro, rl = rf.forward(np32(q), np32(k), np32(v), **okw)
+    # the floor sets the LSE of many rows (log(k 1e-30), about -69, instead of about -96)
+    assert np.sum(np.abs(rl - np.log(1e-30)) < 1.0) > 50 and np.nanmin(rl) < -90
+    assert_parity(o, ro, lse, rl, f"tile floor {dtype} D{D}")
+
+
 def test_kv_cache_offset():
     require_gpu()
     B, H, D = 2, 4, 128
