@@ -101,7 +101,7 @@ def _draw_long(n: int, seed: int):
     return cases
 
 
-LONG_CASES = _draw_long(16, 20261205)
+LONG_CASES = _draw_long(24, 20261205)
 
 
 @pytest.mark.parametrize("case", LONG_CASES, ids=[c[0] for c in LONG_CASES])
@@ -138,6 +138,54 @@ def test_backward_sweep(case):
                                softcap=softcap, q_offset=0)
     o = torch.from_numpy(o32).to(dt)
     say(f"backward sweep {name}")
+    dq, dk, dv = ffa.fastest_flash_attn_backward(
+        do.cuda(), q.cuda(), k.cuda(), v.cuda(), o.cuda(), torch.from_numpy(lse).cuda(),
+        scale=scale, causal=causal, softcap=softcap, sliding_window=window)
+    torch.cuda.synchronize()
+    rq, rk, rv = rb.backward(np32(do), np32(q), np32(k), np32(v), np32(o), lse, scale=scale,
+                             causal=causal, softcap=softcap, sliding_window=window)
+    _check(dq, rq, dt, f"{name} dq")
+    _check(dk, rk, dt, f"{name} dk")
+    _check(dv, rv, dt, f"{name} dv")
+
+
+def _draw_bwd_long(n: int, seed: int):
+    """Backward sweeps long enough for the kernels' interior tiles, with wide scales."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        D = int(rng.choice((64, 128, 192, 256)))
+        dt = (torch.bfloat16, torch.float16)[int(rng.integers(2))]
+        Hkv = int(rng.choice((1, 2)))
+        Hq = Hkv * int(rng.choice((1, 2)))
+        Sq = int(rng.integers(500, 1000))
+        Skv = Sq if rng.random() < 0.6 else int(rng.integers(500, 1000))
+        causal = bool(rng.random() < 0.6)
+        window = int(rng.integers(100, 500)) if rng.random() < 0.3 else None
+        softcap = float(rng.choice((20.0, 50.0))) if rng.random() < 0.4 else None
+        scale = float(rng.choice((-1.0, -1.0 / math.sqrt(D), 1.0 / math.sqrt(D), 1.0)))
+        name = (f"{i}_H{Hq}-{Hkv}_S{Sq}x{Skv}_D{D}_{str(dt)[6:]}_c{int(causal)}_w{window}"
+                f"_cap{softcap}_s{scale:.3g}")
+        cases.append((name, Hq, Hkv, Sq, Skv, D, dt, causal, window, softcap, scale))
+    return cases
+
+
+BWD_LONG_CASES = _draw_bwd_long(12, 20261206)
+
+
+@pytest.mark.parametrize("case", BWD_LONG_CASES, ids=[c[0] for c in BWD_LONG_CASES])
+def test_backward_sweep_long(case):
+    require_gpu()
+    name, Hq, Hkv, Sq, Skv, D, dt, causal, window, softcap, scale = case
+    seed = 19 + 23 * int(name.split("_")[0])
+    q = seeded((1, Hq, Sq, D), dt, seed)
+    k = seeded((1, Hkv, Skv, D), dt, seed + 1)
+    v = seeded((1, Hkv, Skv, D), dt, seed + 2)
+    do = seeded((1, Hq, Sq, D), dt, seed + 3)
+    o32, lse = _oracle_forward(q, k, v, scale=scale, causal=causal, window=window,
+                               softcap=softcap, q_offset=0)
+    o = torch.from_numpy(o32).to(dt)
+    say(f"backward sweep long {name}")
     dq, dk, dv = ffa.fastest_flash_attn_backward(
         do.cuda(), q.cuda(), k.cuda(), v.cuda(), o.cuda(), torch.from_numpy(lse).cuda(),
         scale=scale, causal=causal, softcap=softcap, sliding_window=window)
