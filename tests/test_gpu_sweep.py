@@ -243,6 +243,36 @@ def test_paged_decode_sweep(case):
             assert torch.all(o[b] == 0) and torch.all(torch.isneginf(lse[b]))
 
 
+DEC_WIDE_CASES = [
+    # (name, lens, Hq, Hkv, D, P, dtype, window, softcap, tps, scale): scores spanning a
+    # wide range, so the split kernel's running max moves and rescales often
+    ("neg3", [900, 37, 1400], 8, 2, 128, 16, torch.bfloat16, None, None, 256, -3.0),
+    ("pos3_softcap", [1200, 600], 8, 8, 64, 16, torch.float16, None, 50.0, 0, 3.0),
+    ("neg3_softcap_window", [1500, 800], 16, 2, 128, 12, torch.bfloat16, 300, 50.0, 64, -3.0),
+    ("pos1_d256", [700, 1300], 4, 1, 256, 32, torch.bfloat16, None, None, 0, 1.0),
+]
+
+
+@pytest.mark.parametrize("case", DEC_WIDE_CASES, ids=[c[0] for c in DEC_WIDE_CASES])
+def test_paged_decode_wide_scores(case):
+    require_gpu()
+    from oracle import paged as opaged
+    from tests.test_gpu_decode import _build_pool
+
+    name, lens, Hq, Hkv, D, P, dt, window, softcap, tps, scale = case
+    k_pages, v_pages, bt = _build_pool(lens, Hkv, D, P, dt, seed=300 + len(name))
+    q = seeded((len(lens), Hq, D), dt, 400 + len(name))
+    kw = dict(sliding_window=window, softcap=softcap, scale=scale)
+    say(f"decode wide scores {name}")
+    o, lse = ffa.fastest_flash_paged_decode(q.cuda(), k_pages.cuda(), v_pages.cuda(), bt.cuda(),
+                                            torch.tensor(lens, dtype=torch.int32).cuda(),
+                                            return_lse=True, tokens_per_split=tps or None, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o).all()
+    ro, rl = opaged.paged_decode(np32(q), np32(k_pages), np32(v_pages), bt.numpy(), lens, **kw)
+    assert_parity(o, ro, lse, rl, name)
+
+
 def _draw_narrow(n: int, seed: int):
     """V narrower than q / k (taken as zero-padded to D): the narrow-V kernels for
     16-bit inputs at head_dim 129..192 with V dims <= 128 and a multiple of 8, the
