@@ -5,8 +5,10 @@
 // q_offset, GQA head map h -> h / (Hq / Hkv), natural-log LSE.
 //
 // Work decomposition: one workgroup (4 waves, 256 threads) per (batch, q-head, 128-row
-// query tile); each wave owns 32 query rows for the whole KV sweep. Inputs must be
-// 16-byte aligned with head_dim % 8 == 0 (the host pads / copies otherwise).
+// query tile); each wave owns 32 query rows for the whole KV sweep. The narrow-V
+// kernels on sequences of 4096 rows or more use 8 waves and 256-row tiles instead.
+// Inputs must be 16-byte aligned with head_dim % 8 == 0 (the host pads / copies
+// otherwise).
 //
 // Per KV tile of BN keys (BN = 64 for head_dim <= 128, 32 above):
 //   S^T[key, q] = K Q^T   v_mfma_f32_32x32x16 with K (LDS) as A and Q (registers) as B,
@@ -14,6 +16,8 @@
 //                         needs one lane swap (l ^ 32), the row sum none until the end.
 //   P = exp2(S*c - m*c)   fp32 (c = scale*log2e, one FMA per score); m moves only when
 //                         the max grows by more than 2^8, so O and l are rarely rescaled.
+//                         The reference's per-tile 1e-30 floor of the row sum is added
+//                         at the end (ref_tile_floor, masked_row_lse).
 //   O^T[d, q] += V^T P^T  B = P packed to 16 bit straight from the S^T accumulators;
 //                         A = V^T from LDS by two ds_read_b64_tr_b16 (4 keys x 1 dim per
 //                         lane each) on the row-major V tile: the key order they produce
