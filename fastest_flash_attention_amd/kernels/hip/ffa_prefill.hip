@@ -776,19 +776,45 @@ __global__ __launch_bounds__((64 * NW), (kMinBlocks<DP, SOFTCAP> * 4 / NW)) void
     if (l_tot > 0.0f) ref_tile_floor(p, qrow, lse, inv);
     uint16_t* orow = p.o + b * p.o_sb + h * p.o_sh + static_cast<int64_t>(qrow) * p.o_ss;
     const int Dv = NARROW ? p.Dv : D;
-#pragma unroll
-    for (int db = 0; db < SV::DB; ++db) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d0 = 32 * db + 8 * i + 4 * g;
-        const uint32_t w0 = E::pack2(oacc[db][4 * i + 0] * inv, oacc[db][4 * i + 1] * inv);
-        const uint32_t w1 = E::pack2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
-        if (d0 < Dv) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{w0, w1};
-      }
-    }
-    // a V narrower than head_dim is zero-padded: O's dims past it are 0
     if constexpr (NARROW) {
-      for (int d0 = Dv + 4 * g; d0 < D; d0 += 8) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{0u, 0u};
+      // Lane (row, g) holds dims 32 db + 8 i + 4 g .. +3. A v_permlane32_swap per dword
+      // gives lane g = 0 both halves of the 8-dim chunks i = 0, 2 and lane g = 1 those of
+      // i = 1, 3, so every store is 16 contiguous bytes (half as many stores, each row's
+      // 32 bytes per instruction in one piece). On MI355X +5-8 % at the MLA prefill
+      // shapes with the zero padding below stored the same way; in the equal-width
+      // kernels it measured within noise and is not used there.
+#pragma unroll
+      for (int db = 0; db < SV::DB; ++db) {
+        uint32_t w[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w[i][0] = E::pack2(oacc[db][4 * i + 0] * inv, oacc[db][4 * i + 1] * inv);
+          w[i][1] = E::pack2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
+        }
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const auto x0 = __builtin_amdgcn_permlane32_swap(w[2 * k][0], w[2 * k + 1][0], false, false);
+          const auto x1 = __builtin_amdgcn_permlane32_swap(w[2 * k][1], w[2 * k + 1][1], false, false);
+          const int d0 = 32 * db + 16 * k + 8 * g;
+          if (d0 < Dv) *reinterpret_cast<u32x4*>(orow + d0) = u32x4{x0[0], x1[0], x0[1], x1[1]};
+        }
+      }
+      // a V narrower than head_dim is zero-padded: O's dims past it are 0 (D and Dv are
+      // multiples of 8, so each 16-byte store ends at or before D)
+      for (int d0 = Dv + 8 * g; d0 < D; d0 += 16) {
+        *reinterpret_cast<u32x4*>(orow + d0) = u32x4{0u, 0u, 0u, 0u};
+      }
+    } else {
+#pragma unroll
+      for (int db = 0; db < SV::DB; ++db) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = 32 * db + 8 * i + 4 * g;
+          const uint32_t w0 = E::pack2(oacc[db][4 * i + 0] * inv, oacc[db][4 * i + 1] * inv);
+          const uint32_t w1 = E::pack2(oacc[db][4 * i + 2] * inv, oacc[db][4 * i + 3] * inv);
+          if (d0 < Dv) *reinterpret_cast<u32x2*>(orow + d0) = u32x2{w0, w1};
+        }
+      }
     }
     if (p.lse != nullptr && g == 0) {
       p.lse[b * p.l_sb + h * p.l_sh + static_cast<int64_t>(qrow) * p.l_ss] = lse;
