@@ -559,11 +559,12 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const DecodeParams p) 
 // Workgroup = 4 waves for (sequence, 32-head group) x split, two workgroups per CU.
 // 32-key tiles of the shared rows go HBM -> LDS (asm global_load_lds_dwordx4) into a
 // 2-stage ring. Wave w takes heads 16 * (w >> 1) + 0..15 (MFMA columns) and output dims
-// [(w & 1) DV/2, (w & 1 + 1) DV/2): it computes S^T = K Q^T for its 16 heads with
-// v_mfma_f32_16x16x32 (the 2 waves of a head group duplicate this small product rather
-// than exchanging P), fp32 softmax with exp2 and deferred rescale, and O^T += V^T P^T
-// with one v_mfma_f32_16x16x32 per 16 dims of its DV/2 (V^T by ds_read_b64_tr_b16).
-// Normalised (O, lse) partials per split are merged by decode_combine_kernel.
+// [(w & 1) DV/2, (w & 1 + 1) DV/2): it computes S^T = K Q^T for its 16 heads and one of
+// the tile's two 16-key blocks with v_mfma_f32_16x16x32 (the other block comes from the
+// partner wave of its head group through LDS), fp32 softmax with exp2 and deferred
+// rescale, and O^T += V^T P^T with one v_mfma_f32_16x16x32 per 16 dims of its DV/2 (V^T
+// by ds_read_b64_tr_b16). Normalised (O, lse) partials per split are merged by
+// mla_combine_kernel (up to 16 splits) or decode_combine_kernel.
 // ---------------------------------------------------------------------------------
 constexpr int kMlaWaves = 4;
 constexpr int kMlaThreads = 64 * kMlaWaves;
@@ -619,8 +620,13 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   constexpr int DBW = DW / 16;                 // 16-dim output blocks per wave
   static_assert(CH % 8 == 0 && kMlaTile * CH % kMlaThreads == 0, "row / tile shape");
   __shared__ __attribute__((aligned(1024))) uint16_t ring[kMlaStages][TILE];
-  __shared__ int bt_lds[kMlaMaxSplit + 2];
-  __shared__ int bad_lds[kMlaWaves];
+  // Split starts are multiples of the 32-token tile and splits hold at most kMlaMaxSplit
+  // tokens, so a split spans at most kMlaMaxSplit pages (page size 1).
+  __shared__ int bt_lds[kMlaMaxSplit];
+  // Each wave's S^T key block for its partner wave (below); before the sweep, the
+  // waves' invalid-page votes. 80 KiB in all: two workgroups per CU.
+  __shared__ __attribute__((aligned(16))) f32x4 xbuf[kMlaWaves][64];
+  int* const bad_lds = reinterpret_cast<int*>(&xbuf[0][0]);
 
   // blockIdx.x = (sequence, head group), blockIdx.y = split (XCD balance, as in the
   // paged decode kernel)
@@ -756,38 +762,35 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
 
   auto compute = [&](int t, const uint16_t* tl) {
     const int t0 = s_begin + t * kMlaTile;
-    // S^T in four interleaved accumulator chains (key block kb x even / odd k-step),
-    // the K operands read one k-step ahead of their MFMAs: with one wave per SIMD
-    // nothing else hides the LDS and MFMA latencies of a single dependent chain.
+    // S^T of the tile's two 16-key blocks: wave (hs, dq) computes block kb = dq for its
+    // head group (even / odd k-steps in two accumulator chains, the K operands read one
+    // k-step ahead) and takes the other block from its partner wave (hs, 1 - dq) through
+    // LDS, so each K byte is read from LDS by two waves instead of four. The exchange
+    // barrier is also what lets the next tile's loads be issued at the top of the
+    // sweep (one barrier fewer per tile). On MI355X -3 % per cfg5 step, bit-identical.
     auto k_at = [&](int ks, int kb) {
       return *reinterpret_cast<const u32x4*>(tl + ((ks & 1) ? k_rd1 : k_rd0) + (ks >> 1) * 64 +
                                              kb * 16 * DQK);
     };
-    f32x4 sp[2][2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sp[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      sp[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    u32x4 a_cur[2] = {k_at(0, 0), k_at(0, 1)};
+    f32x4 sp[2];
+    sp[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    sp[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 a_cur = k_at(0, dq);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      u32x4 a_nxt[2];
-      if (ks + 1 < KS) {
-        a_nxt[0] = k_at(ks + 1, 0);
-        a_nxt[1] = k_at(ks + 1, 1);
-      }
+      u32x4 a_nxt;
+      if (ks + 1 < KS) a_nxt = k_at(ks + 1, dq);
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) sp[kb][ks & 1] = E::mfma16(a_cur[kb], qreg[ks], sp[kb][ks & 1]);
-      if (ks + 1 < KS) {
-        a_cur[0] = a_nxt[0];
-        a_cur[1] = a_nxt[1];
-      }
+      sp[ks & 1] = E::mfma16(a_cur, qreg[ks], sp[ks & 1]);
+      if (ks + 1 < KS) a_cur = a_nxt;
     }
+    const f32x4 own = sp[0] + sp[1];
+    xbuf[wave][lane] = own;
+    __syncthreads();  // both blocks of every head group are in xbuf
+    const f32x4 other = xbuf[wave ^ 1][lane];
     f32x4 sacc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) sacc[kb] = sp[kb][0] + sp[kb][1];
+    sacc[0] = dq == 0 ? own : other;
+    sacc[1] = dq == 0 ? other : own;
     // S^T lane layout: keys 16 kb + 4 g4 + j of head c16
     const bool tile_ok = !TILE_PAGE || !any_bad || tile_page(t0) >= 0;  // uniform
     float mt = kNegInf;
@@ -844,30 +847,16 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
     }
   };
 
-  // kMlaStages-deep ring: tiles t + 1 .. t + kMlaStages - 1 stay in flight while tile t
-  // is computed (the vmcnt counter retires loads in order, so waiting until at most
-  // `ahead` tiles' loads remain leaves tile t complete).
-  static_assert(kMlaStages >= 2 && kMlaStages <= 4 && (kMlaStages - 1) * LPT < 64, "vmcnt range");
-  for (int t = 0; t < kMlaStages && t < n_tiles; ++t) issue(t, t);
-  int st = 0;
+  // Two-stage ring: tile t + 1 is in flight while tile t is computed. The barrier at the
+  // top of iteration t both publishes tile t and shows every wave done with tile t - 1,
+  // whose stage tile t + 1 then refills.
+  static_assert(kMlaStages == 2 && LPT < 64, "two-stage ring, vmcnt range");
+  if (n_tiles > 0) issue(0, 0);
   for (int t = 0; t < n_tiles; ++t) {
-    const int ahead = min(kMlaStages - 1, n_tiles - 1 - t);
-    if (ahead >= 3) {
-      wait_vmcnt<3 * LPT>();
-    } else if (ahead == 2) {
-      wait_vmcnt<2 * LPT>();
-    } else if (ahead == 1) {
-      wait_vmcnt<LPT>();
-    } else {
-      wait_vmcnt0();
-    }
-    __syncthreads();  // tile t is in LDS
-    compute(t, ring[st]);
-    if (t + kMlaStages < n_tiles) {
-      __syncthreads();  // every wave is done with stage st
-      issue(t + kMlaStages, st);
-    }
-    st = st + 1 == kMlaStages ? 0 : st + 1;
+    wait_vmcnt0();
+    __syncthreads();  // tile t is in LDS; every wave is done with stage (t + 1) & 1
+    if (t + 1 < n_tiles) issue(t + 1, (t + 1) & 1);
+    compute(t, ring[t & 1]);
   }
 
   // Partial of this split: O^T lane layout dims 16 db + 4 g4 + j (of this wave's
