@@ -49,6 +49,9 @@ MLA_CASES = [
     (BF16, 512, 8, 16, [1024, 3], 1024),
     (BF16, 256, 1, 1, [45, 9], 32),
     (BF16, 256, 32, 32, [700, 64, 33, 1], None),  # whole-tile page path at dim_v 256
+    # one-token pages with the largest split: a split spans 1024 pages, every entry of
+    # the kernel's staged block table
+    (BF16, 512, 16, 1, [2053, 1030], 1024),
 ]
 
 
