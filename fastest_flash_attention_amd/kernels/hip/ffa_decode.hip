@@ -124,13 +124,13 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
   static_assert(kTile * CPR % 64 == 0, "tile rows must fill whole wave loads");
   // Per wave: 2 stages x (K tile, V tile); reused for the wave merge afterwards.
   constexpr int kStageBytes = kDecWaves * 2 * 2 * TILE * 2;
-  constexpr int kRedBytes = kDecWaves * kCols * (DP + 1) * 4;
+  constexpr int kRedBytes = kDecWaves * kCols * (DP + 4) * 4;
   __shared__ __attribute__((aligned(1024))) char smem[kStageBytes > kRedBytes ? kStageBytes : kRedBytes];
   __shared__ int bt_lds[kMaxSplit + 2];
   __shared__ int bad_lds[kDecWaves];
   __shared__ float red_m[kDecWaves][kCols];
   __shared__ float red_l[kDecWaves][kCols];
-  auto red_o = reinterpret_cast<float(*)[kCols][DP + 1]>(smem);
+  auto red_o = reinterpret_cast<float(*)[kCols][DP + 4]>(smem);
 
   // blockIdx.x = (sequence, KV head, column group), blockIdx.y = split: workgroups are
   // dealt to the 8 XCDs round-robin by linear id, so every XCD gets whole KV heads of
@@ -355,35 +355,54 @@ __global__ __launch_bounds__(kDecThreads, kDecMinBlocks<DP>) void decode_split_k
     red_m[wave][c16] = m_run;
     red_l[wave][c16] = l_w;
   }
+  if (c16 < gcols) {
 #pragma unroll
-  for (int db = 0; db < S::DB; ++db) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red_o[wave][c16][16 * db + 4 * g4 + j] = oacc[db][j];
+    for (int db = 0; db < S::DB; ++db) {
+      *reinterpret_cast<f32x4*>(&red_o[wave][c16][16 * db + 4 * g4]) = oacc[db];
+    }
   }
   __syncthreads();
 
-  // thread -> (column, dim) pairs of the merged partial
-  for (int idx = tid; idx < kCols * DP; idx += kDecThreads) {
-    const int n = idx / DP;
-    const int d = idx - n * DP;
-    if (n >= gcols) continue;
+  // Merge of the four waves' partials: 16 threads per column n (query head), 8
+  // consecutive dims each, the waves' weights computed once per thread; 16-byte LDS
+  // reads and workspace stores (rows are padded by 4 floats, keeping them 16-byte
+  // aligned).
+  const int n = tid >> 4;
+  if (n < gcols) {
     float mm = kNegInf;
 #pragma unroll
     for (int w = 0; w < kDecWaves; ++w) mm = fmaxf(mm, red_m[w][n]);
+    float wt[kDecWaves];
     float lsum = 0.0f;
-    float osum = 0.0f;
-    if (mm != kNegInf) {
 #pragma unroll
-      for (int w = 0; w < kDecWaves; ++w) {
-        const float wt = fast_exp2(red_m[w][n] - mm);
-        lsum += wt * red_l[w][n];
-        osum += wt * red_o[w][n][d];
-      }
+    for (int w = 0; w < kDecWaves; ++w) {
+      wt[w] = mm != kNegInf ? fast_exp2(red_m[w][n] - mm) : 0.0f;
+      lsum += wt[w] * red_l[w][n];
     }
     const int hq = head0 + n;
     const int64_t slot = (static_cast<int64_t>(b) * p.Hq + hq) * p.n_splits + split;
-    if (d < D) p.ws_o[slot * p.dp + d] = lsum > 0.0f ? osum / lsum : 0.0f;
-    if (d == 0) p.ws_lse[slot] = lsum > 0.0f ? (mm + fast_log2(lsum)) * kLn2 : kNegInf;
+    for (int d0 = (tid & 15) * 8; d0 < D; d0 += 128) {
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(&red_o[w][n][d0]);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(&red_o[w][n][d0 + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] += wt[w] * x0[e];
+          o[4 + e] += wt[w] * x1[e];
+        }
+      }
+      f32x4 r0, r1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r0[e] = lsum > 0.0f ? o[e] / lsum : 0.0f;
+        r1[e] = lsum > 0.0f ? o[4 + e] / lsum : 0.0f;
+      }
+      *reinterpret_cast<f32x4*>(p.ws_o + slot * p.dp + d0) = r0;
+      *reinterpret_cast<f32x4*>(p.ws_o + slot * p.dp + d0 + 4) = r1;
+    }
+    if ((tid & 15) == 0) p.ws_lse[slot] = lsum > 0.0f ? (mm + fast_log2(lsum)) * kLn2 : kNegInf;
   }
 }
 
