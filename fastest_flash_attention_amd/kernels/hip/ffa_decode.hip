@@ -575,7 +575,9 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const DecodeParams p) 
 //
 // Pool layout: [num_pages, page_size, DV + 64], token t of sequence b at page
 // block_tables[b][t / page_size], slot t % page_size (the PagedKVCache index law).
-// Workgroup = 4 waves for (sequence, 32-head group) x split, two workgroups per CU.
+// Two kernels: this four-wave one serves latent 256, the eight-wave one further down
+// latent 512. Four-wave workgroup = 4 waves for (sequence, 32-head group) x split, two
+// workgroups per CU.
 // 32-key tiles of the shared rows go HBM -> LDS (asm global_load_lds_dwordx4) into a
 // 2-stage ring. Wave w takes heads 16 * (w >> 1) + 0..15 (MFMA columns) and output dims
 // [(w & 1) DV/2, (w & 1 + 1) DV/2): it computes S^T = K Q^T for its 16 heads and one of
@@ -623,11 +625,9 @@ __device__ inline int mla_page_of(const MlaParams& p, int tok, int& slot) {
 // rows of a K operand read, and the 4 rows of a transposed V read, over distinct banks.
 __device__ inline int mla_swz(int r) { return (r >> 1) & 7; }
 
-// TILE_PAGE: page_size is a multiple of the 32-token tile, so a tile (they start at
-// multiples of 32) never straddles a page: one wave-uniform page lookup per tile, and
-// each load is the tile's base (SGPRs) plus a per-lane 32-bit offset fixed for the whole
-// sweep. Otherwise every row of a tile finds its own page.
-template <typename Tag, int DV, bool TILE_PAGE>
+// Every row of a tile finds its own page (per-row page lookups; the whole-tile page
+// path of the eight-wave kernel is not used at latent 256, see launch_mla_tag).
+template <typename Tag, int DV>
 __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const MlaParams p) {
   using E = Elem<Tag>;
   constexpr int DQK = DV + kMlaRope;
@@ -701,58 +701,21 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
 
   const char* pool = reinterpret_cast<const char*>(p.kv);
   const int n_tiles = (s_end - s_begin + kMlaTile - 1) / kMlaTile;
-  // Load j of this lane fills chunk position P = (4j + wave) * 64 + lane of a tile.
-  // Load j of this lane: tile row ld_row(j), byte offset ld_off[j] of its swizzled
-  // chunk inside the tile's rows (rows are contiguous within a page).
-  auto ld_row = [&](int j) { return ((4 * j + wave) * 64 + lane) / CH; };
-  uint32_t ld_off[LPT];
-#pragma unroll
-  for (int j = 0; j < LPT; ++j) {
-    const int pos = (4 * j + wave) * 64 + lane;
-    const int row = pos / CH;
-    const int pc = pos - row * CH;
-    ld_off[j] = static_cast<uint32_t>(row * DQK * 2 + (pc ^ mla_swz(row)) * 16);
-  }
-  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + wave * 1024);
-  // Page id of tile t (TILE_PAGE): wave-uniform; -1 for an id outside the pool.
-  auto tile_page = [&](int t0) {
-    int slot;
-    const int pg = mla_page_of(p, t0, slot);
-    return __builtin_amdgcn_readfirstlane(bt_lds[pg - pg0]);
-  };
+  // Load j of this lane fills chunk position (4j + wave) * 64 + lane of a tile: row
+  // pos / CH of the tile, its swizzled 16-byte chunk, from that row's own page.
   auto issue = [&](int t, int st) {
     const int t0 = s_begin + t * kMlaTile;
-    if constexpr (TILE_PAGE) {
+    uint16_t* dst = ring[st];
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int pos = (4 * j + wave) * 64 + lane;
+      const int row = pos / CH;
+      const int pc = pos - row * CH;
+      const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
       int slot;
-      mla_page_of(p, t0, slot);
-      const int phys = max(tile_page(t0), 0);
-      const char* tb = pool + (static_cast<int64_t>(phys) * p.P + slot) * DQK * 2;
-      const uint32_t dst = ring_lds + st * TILE * 2;
-      if (t0 + kMlaTile <= s_end) {
-#pragma unroll
-        for (int j = 0; j < LPT; ++j) load_lds16_async(tb, ld_off[j], dst + j * 4096);
-      } else {
-        // last tile of the split: rows past s_end - 1 re-read that row (masked)
-        const int last = s_end - 1 - t0;
-#pragma unroll
-        for (int j = 0; j < LPT; ++j) {
-          const uint32_t back = static_cast<uint32_t>(max(0, ld_row(j) - last) * DQK * 2);
-          load_lds16_async(tb, ld_off[j] - back, dst + j * 4096);
-        }
-      }
-    } else {
-      uint16_t* dst = ring[st];
-#pragma unroll
-      for (int j = 0; j < LPT; ++j) {
-        const int pos = (4 * j + wave) * 64 + lane;
-        const int row = pos / CH;
-        const int pc = pos - row * CH;
-        const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
-        int slot;
-        const int pg = mla_page_of(p, tok, slot);
-        const int64_t ro = (static_cast<int64_t>(max(bt_lds[pg - pg0], 0)) * p.P + slot) * DQK * 2;
-        load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (4 * j + wave) * 512));
-      }
+      const int pg = mla_page_of(p, tok, slot);
+      const int64_t ro = (static_cast<int64_t>(max(bt_lds[pg - pg0], 0)) * p.P + slot) * DQK * 2;
+      load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (4 * j + wave) * 512));
     }
   };
 
@@ -811,15 +774,14 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
     sacc[0] = dq == 0 ? own : other;
     sacc[1] = dq == 0 ? other : own;
     // S^T lane layout: keys 16 kb + 4 g4 + j of head c16
-    const bool tile_ok = !TILE_PAGE || !any_bad || tile_page(t0) >= 0;  // uniform
     float mt = kNegInf;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tok = t0 + 16 * kb + 4 * g4 + j;
-        bool live = tok < s_end && tile_ok;
-        if (!TILE_PAGE && any_bad && live) {
+        bool live = tok < s_end;
+        if (any_bad && live) {
           int slot;
           live = bt_lds[mla_page_of(p, tok, slot) - pg0] >= 0;
         }
@@ -888,6 +850,278 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
   // A normalised partial is a convex combination of latent rows, so it fits the
   // input's 16-bit type: half the partial traffic of fp32 (both the write here and the
   // combine's read).
+  uint16_t* wo = p.ws_o + row * DV + dq * DW + 4 * g4;
+#pragma unroll
+  for (int db = 0; db < DBW; ++db) {
+    const u32x2 v = {E::pack2(oacc[db][0] * inv, oacc[db][1] * inv),
+                     E::pack2(oacc[db][2] * inv, oacc[db][3] * inv)};
+    *reinterpret_cast<u32x2*>(wo + 16 * db) = v;
+  }
+  if (dq == 0 && g4 == 0) {
+    p.ws_lse[row] = l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : kNegInf;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Eight-wave MLA split kernel (latent 512): two waves per SIMD. Wave w takes head
+// subgroup hs = w >> 2 (16 heads as MFMA columns) and output quarter dq = w & 3 (128
+// latent dims). S^T of a 32-token tile is cut into four pieces per head subgroup: key
+// block kb = dq & 1 over k-step half kh = dq >> 1 (9 of the 18 k-steps); each wave
+// computes its piece and the four are summed from LDS as (kh 0 + kh 1) in every wave
+// of the subgroup, so the subgroup's waves hold identical scores and softmax state.
+// Per tile a wave issues 9 S^T MFMAs and 8 P.V MFMAs against 18 and 16 at four waves,
+// with the same LDS operand bytes per workgroup. 84 KiB of LDS (ring, staged block
+// table, 8 KiB of pieces): one workgroup, eight waves, per CU.
+// TILE_PAGE: page_size is a multiple of the 32-token tile, so a tile (they start at
+// multiples of 32) never straddles a page: one wave-uniform page lookup per tile, and
+// each load is the tile's base (SGPRs) plus a per-lane 32-bit offset fixed for the whole
+// sweep. Otherwise every row of a tile finds its own page.
+// ---------------------------------------------------------------------------------
+constexpr int kMla8Waves = 8;
+constexpr int kMla8Threads = 64 * kMla8Waves;
+
+template <typename Tag, bool TILE_PAGE>
+__global__ __launch_bounds__(kMla8Threads, 1) void mla_decode_split8_kernel(const MlaParams p) {
+  using E = Elem<Tag>;
+  constexpr int DV = 512;
+  constexpr int DQK = DV + kMlaRope;             // 576
+  constexpr int CH = DQK / 8;                    // 72 chunks per row
+  constexpr int TILE = kMlaTile * DQK;           // elements per tile
+  constexpr int NPOS = kMlaTile * CH;            // 2304 chunk positions per tile
+  constexpr int LPT = NPOS / kMla8Threads;       // 4 loads per lane per tile ...
+  constexpr int XW = (NPOS - LPT * kMla8Threads) / 64;  // ... and one more in waves 0..XW-1
+  static_assert((NPOS - LPT * kMla8Threads) % 64 == 0 && XW < kMla8Waves, "tile split");
+  constexpr int KS = DQK / 32;                   // 18 k-steps
+  constexpr int KH = KS / 2;                     // per k-step half
+  static_assert(KS % 2 == 0, "k-step halves");
+  constexpr int DW = DV / 4;                     // 128 output dims per wave
+  constexpr int DBW = DW / 16;                   // 8 dim blocks per wave
+  __shared__ __attribute__((aligned(1024))) uint16_t ring[2][TILE];
+  __shared__ int bt_lds[kMlaMaxSplit];
+  __shared__ __attribute__((aligned(16))) f32x4 xbuf[kMla8Waves][64];
+  int* const bad_lds = reinterpret_cast<int*>(&xbuf[0][0]);
+
+  const int split = blockIdx.y;
+  const int b = blockIdx.x / p.n_hg;
+  const int hg = blockIdx.x - b * p.n_hg;
+  const int L = min(max(p.lens[b], 0), p.max_len);
+  const int s_begin = split * p.tps;
+  const int s_end = min(s_begin + p.tps, L);
+  if (s_begin >= s_end) return;  // uniform across the workgroup: no barrier reached
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int c16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int hs = wave >> 2;  // head subgroup: MFMA columns = heads 16 hs + c16
+  const int dq = wave & 3;   // output dim quarter
+  const int kb = dq & 1;     // S^T key block of this wave's piece
+  const int kh = dq >> 1;    // S^T k-step half of this wave's piece
+  const int head = hg * 32 + hs * 16 + c16;
+  const bool head_live = head < p.Hq;
+
+  int slot0;
+  const int pg0 = mla_page_of(p, s_begin, slot0);
+  int slot1;
+  const int pg1 = mla_page_of(p, s_end - 1, slot1);
+  bool bad = false;
+  {
+    const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
+    for (int i = tid; i <= pg1 - pg0; i += kMla8Threads) {
+      const int phys = btrow[pg0 + i];
+      const bool ok = phys >= 0 && phys < p.num_pages;
+      bt_lds[i] = ok ? phys : -1;
+      bad = bad || !ok;
+    }
+  }
+  const bool wave_bad = __any(bad);
+  if (lane == 0) bad_lds[wave] = wave_bad ? 1 : 0;
+  // Q^T as the B operand for this wave's k-steps: lane holds head `head`, dims
+  // 32 (KH kh + i) + 8 g4 .. +7.
+  u32x4 qreg[KH];
+  {
+    const uint16_t* qr = p.q + b * p.q_sb + static_cast<int64_t>(head_live ? head : 0) * p.q_sh;
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + 32 * (KH * kh + i) + 8 * g4);
+      qreg[i] = head_live ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  wait_vmcnt0();
+  __syncthreads();
+  bool any_bad = false;
+#pragma unroll
+  for (int w = 0; w < kMla8Waves; ++w) any_bad = any_bad || bad_lds[w] != 0;
+
+  const char* pool = reinterpret_cast<const char*>(p.kv);
+  const int n_tiles = (s_end - s_begin + kMlaTile - 1) / kMlaTile;
+  // Load j of this lane fills chunk position (8 j + wave) * 64 + lane of a tile (load
+  // LPT only in waves 0 .. XW - 1).
+  auto ld_pos = [&](int j) { return (kMla8Waves * j + wave) * 64 + lane; };
+  uint32_t ld_off[LPT + 1];
+#pragma unroll
+  for (int j = 0; j <= LPT; ++j) {
+    const int pos = min(ld_pos(j), NPOS - 1);
+    const int row = pos / CH;
+    const int pc = pos - row * CH;
+    ld_off[j] = static_cast<uint32_t>(row * DQK * 2 + (pc ^ mla_swz(row)) * 16);
+  }
+  const bool extra = wave < XW;  // wave-uniform
+  const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(&ring[0][0]) + wave * 1024);
+  auto tile_page = [&](int t0) {
+    int slot;
+    const int pg = mla_page_of(p, t0, slot);
+    return __builtin_amdgcn_readfirstlane(bt_lds[pg - pg0]);
+  };
+  auto issue = [&](int t, int st) {
+    const int t0 = s_begin + t * kMlaTile;
+    if constexpr (TILE_PAGE) {
+      int slot;
+      mla_page_of(p, t0, slot);
+      const int phys = max(tile_page(t0), 0);
+      const char* tb = pool + (static_cast<int64_t>(phys) * p.P + slot) * DQK * 2;
+      const uint32_t dst = ring_lds + st * TILE * 2;
+      if (t0 + kMlaTile <= s_end) {
+#pragma unroll
+        for (int j = 0; j < LPT; ++j) load_lds16_async(tb, ld_off[j], dst + j * 1024 * kMla8Waves);
+        if (extra) load_lds16_async(tb, ld_off[LPT], dst + LPT * 1024 * kMla8Waves);
+      } else {
+        // last tile of the split: rows past s_end - 1 re-read that row (masked)
+        const int last = s_end - 1 - t0;
+#pragma unroll
+        for (int j = 0; j <= LPT; ++j) {
+          if (j == LPT && !extra) break;
+          const uint32_t back = static_cast<uint32_t>(max(0, ld_pos(j) / CH - last) * DQK * 2);
+          load_lds16_async(tb, ld_off[j] - back, dst + j * 1024 * kMla8Waves);
+        }
+      }
+    } else {
+      uint16_t* dst = ring[st];
+#pragma unroll
+      for (int j = 0; j <= LPT; ++j) {
+        if (j == LPT && !extra) break;
+        const int pos = ld_pos(j);
+        const int row = pos / CH;
+        const int pc = pos - row * CH;
+        const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
+        int slot;
+        const int pg = mla_page_of(p, tok, slot);
+        const int64_t ro = (static_cast<int64_t>(max(bt_lds[pg - pg0], 0)) * p.P + slot) * DQK * 2;
+        load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (kMla8Waves * j + wave) * 512));
+      }
+    }
+  };
+
+  const int ksw = mla_swz(c16);
+  const int k_rd0 = c16 * DQK + (((0 + g4) ^ ksw) << 3);
+  const int k_rd1 = c16 * DQK + (((4 + g4) ^ ksw) << 3);
+  const int vrow = 4 * g4 + (c16 >> 2);
+  const int vsw = mla_swz(vrow);
+  int v_rd[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int col = dq * DW + 16 * u + 4 * (c16 & 3);
+    v_rd[u] = vrow * DQK + (((col >> 3) ^ vsw) << 3) + (col & 7);
+  }
+
+  f32x4 oacc[DBW];
+#pragma unroll
+  for (int db = 0; db < DBW; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = kNegInf;
+  float l_run = 0.0f;
+
+  auto compute = [&](int t, const uint16_t* tl) {
+    const int t0 = s_begin + t * kMlaTile;
+    auto k_at = [&](int ks, int kbb) {
+      return *reinterpret_cast<const u32x4*>(tl + ((ks & 1) ? k_rd1 : k_rd0) + (ks >> 1) * 64 +
+                                             kbb * 16 * DQK);
+    };
+    f32x4 sp[2];
+    sp[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    sp[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    u32x4 a_cur = k_at(KH * kh, kb);
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+      u32x4 a_nxt;
+      if (i + 1 < KH) a_nxt = k_at(KH * kh + i + 1, kb);
+      __builtin_amdgcn_sched_barrier(0);
+      sp[i & 1] = E::mfma16(a_cur, qreg[i], sp[i & 1]);
+      if (i + 1 < KH) a_cur = a_nxt;
+    }
+    xbuf[wave][lane] = sp[0] + sp[1];
+    __syncthreads();  // every piece of every head subgroup is in xbuf
+    f32x4 sacc[2];
+#pragma unroll
+    for (int kbb = 0; kbb < 2; ++kbb) {
+      sacc[kbb] = xbuf[4 * hs + kbb][lane] + xbuf[4 * hs + 2 + kbb][lane];
+    }
+    const bool tile_ok = !TILE_PAGE || !any_bad || tile_page(t0) >= 0;  // uniform
+    float mt = kNegInf;
+#pragma unroll
+    for (int kbb = 0; kbb < 2; ++kbb) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tok = t0 + 16 * kbb + 4 * g4 + j;
+        bool live = tok < s_end && tile_ok;
+        if (!TILE_PAGE && any_bad && live) {
+          int slot;
+          live = bt_lds[mla_page_of(p, tok, slot) - pg0] >= 0;
+        }
+        const float x = live ? sacc[kbb][j] * p.score_mul : kNegInf;
+        sacc[kbb][j] = x;
+        mt = fmaxf(mt, x);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = wave_pair_max(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const bool need = m_new > m_run + kRescaleThresh;
+    if (__any(need)) {
+      const float alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
+      m_run = need ? m_new : m_run;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DBW; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) oacc[db][j] *= alpha;
+      }
+    }
+    const float mu = (m_run == kNegInf) ? 0.0f : m_run;
+    u32x2 pk[2];
+#pragma unroll
+    for (int kbb = 0; kbb < 2; ++kbb) {
+      float e[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        e[j] = fast_exp2(sacc[kbb][j] - mu);
+        l_run += e[j];
+      }
+      pk[kbb] = u32x2{E::pack2(e[0], e[1]), E::pack2(e[2], e[3])};
+    }
+    const u32x4 pb = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
+#pragma unroll
+    for (int db = 0; db < DBW; ++db) {
+      const int off = v_rd[db & 3] + (db >> 2) * 64;
+      const u32x2 a0 = lds_read_tr16(tl + off);
+      const u32x2 a1 = lds_read_tr16(tl + off + 16 * DQK);
+      oacc[db] = E::mfma16(u32x4{a0[0], a0[1], a1[0], a1[1]}, pb, oacc[db]);
+    }
+  };
+
+  if (n_tiles > 0) issue(0, 0);
+  for (int t = 0; t < n_tiles; ++t) {
+    wait_vmcnt0();
+    __syncthreads();  // tile t is in LDS; every wave is done with stage (t + 1) & 1
+    if (t + 1 < n_tiles) issue(t + 1, (t + 1) & 1);
+    compute(t, ring[t & 1]);
+  }
+
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot = wave_pair_sum(l_tot);
+  if (!head_live) return;
+  const int64_t row = (static_cast<int64_t>(b) * p.Hq + head) * p.n_splits + split;
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   uint16_t* wo = p.ws_o + row * DV + dq * DW + 4 * g4;
 #pragma unroll
   for (int db = 0; db < DBW; ++db) {
@@ -1214,19 +1448,23 @@ namespace {
 template <typename Tag>
 void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3 grid,
                     hipStream_t s) {
-  // The whole-tile page path serves latent 512 only. Its latent-256 instantiation gave
-  // wrong scores on MI355X (deterministically, for some lanes of one key block: a K
-  // operand read returned the 16 bytes of a later k-step's read) although its LDS tile
-  // and Q registers were verified correct; the per-row page path computes latent 256.
+  // Latent 512 runs the eight-wave kernel: at 32-token-multiple pages it measured the
+  // same as the four-wave one (cfg5, 33.4 against 33.5 us per step), at 16-token pages
+  // (per-row page lookups) 12 % faster (35.8 against 40.6 us). The whole-tile page path
+  // serves latent 512 only: a latent-256 instantiation of it (in the four-wave kernel)
+  // gave wrong scores on MI355X (deterministically, for some lanes of one key block: a
+  // K operand read returned the 16 bytes of a later k-step's read) although its LDS tile
+  // and Q registers were verified correct; latent 256 runs the four-wave kernel with
+  // per-row page lookups.
   const bool tile_page = mp.P % kMlaTile == 0 && dim_v == 512;
   if (dim_v == 512) {
     if (tile_page) {
-      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512, true>), grid, dim3(kMlaThreads), 0, s, mp);
+      hipLaunchKernelGGL((mla_decode_split8_kernel<Tag, true>), grid, dim3(kMla8Threads), 0, s, mp);
     } else {
-      hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 512, false>), grid, dim3(kMlaThreads), 0, s, mp);
+      hipLaunchKernelGGL((mla_decode_split8_kernel<Tag, false>), grid, dim3(kMla8Threads), 0, s, mp);
     }
   } else {
-    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256, false>), grid, dim3(kMlaThreads), 0, s, mp);
+    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256>), grid, dim3(kMlaThreads), 0, s, mp);
   }
   const unsigned heads4 = static_cast<unsigned>((static_cast<int64_t>(cp.B) * cp.Hq + 3) / 4);
   if (cp.n_splits <= 8) {
