@@ -575,22 +575,14 @@ __global__ __launch_bounds__(256) void mla_combine_kernel(const DecodeParams p) 
 //
 // Pool layout: [num_pages, page_size, DV + 64], token t of sequence b at page
 // block_tables[b][t / page_size], slot t % page_size (the PagedKVCache index law).
-// Two kernels: this four-wave one serves latent 256, the eight-wave one further down
-// latent 512. Four-wave workgroup = 4 waves for (sequence, 32-head group) x split, two
-// workgroups per CU.
-// 32-key tiles of the shared rows go HBM -> LDS (asm global_load_lds_dwordx4) into a
-// 2-stage ring. Wave w takes heads 16 * (w >> 1) + 0..15 (MFMA columns) and output dims
-// [(w & 1) DV/2, (w & 1 + 1) DV/2): it computes S^T = K Q^T for its 16 heads and one of
-// the tile's two 16-key blocks with v_mfma_f32_16x16x32 (the other block comes from the
-// partner wave of its head group through LDS), fp32 softmax with exp2 and deferred
-// rescale, and O^T += V^T P^T with one v_mfma_f32_16x16x32 per 16 dims of its DV/2 (V^T
-// by ds_read_b64_tr_b16). Normalised (O, lse) partials per split are merged by
-// mla_combine_kernel (up to 16 splits) or decode_combine_kernel.
+// Workgroup = 8 waves for (sequence, 32-head group) x split (mla_decode_split8_kernel
+// below). 32-key tiles of the shared rows go HBM -> LDS (asm global_load_lds_dwordx4)
+// into a 2-stage ring; S^T = K Q^T on v_mfma_f32_16x16x32, fp32 softmax with exp2 and
+// deferred rescale, O^T += V^T P^T on v_mfma_f32_16x16x32 (V^T by ds_read_b64_tr_b16).
+// Normalised (O, lse) partials per split are merged by mla_combine_kernel (up to 16
+// splits) or decode_combine_kernel.
 // ---------------------------------------------------------------------------------
-constexpr int kMlaWaves = 4;
-constexpr int kMlaThreads = 64 * kMlaWaves;
 constexpr int kMlaTile = 32;
-constexpr int kMlaStages = 2;
 constexpr int kMlaRope = 64;
 constexpr int kMlaMaxSplit = 1024;
 constexpr int kMlaDefaultSplit = 512;
@@ -625,253 +617,18 @@ __device__ inline int mla_page_of(const MlaParams& p, int tok, int& slot) {
 // rows of a K operand read, and the 4 rows of a transposed V read, over distinct banks.
 __device__ inline int mla_swz(int r) { return (r >> 1) & 7; }
 
-// Every row of a tile finds its own page (per-row page lookups; the whole-tile page
-// path of the eight-wave kernel is not used at latent 256, see launch_mla_tag).
-template <typename Tag, int DV>
-__global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const MlaParams p) {
-  using E = Elem<Tag>;
-  constexpr int DQK = DV + kMlaRope;
-  constexpr int CH = DQK / 8;                  // 16-byte chunks per row
-  constexpr int TILE = kMlaTile * DQK;         // elements per tile
-  constexpr int LPT = kMlaTile * CH / kMlaThreads;  // loads per lane per tile
-  constexpr int KS = DQK / 32;                 // QK k-steps
-  constexpr int DW = DV / 2;                   // output dims per wave
-  constexpr int DBW = DW / 16;                 // 16-dim output blocks per wave
-  static_assert(CH % 8 == 0 && kMlaTile * CH % kMlaThreads == 0, "row / tile shape");
-  __shared__ __attribute__((aligned(1024))) uint16_t ring[kMlaStages][TILE];
-  // Split starts are multiples of the 32-token tile and splits hold at most kMlaMaxSplit
-  // tokens, so a split spans at most kMlaMaxSplit pages (page size 1).
-  __shared__ int bt_lds[kMlaMaxSplit];
-  // Each wave's S^T key block for its partner wave (below); before the sweep, the
-  // waves' invalid-page votes. 80 KiB in all: two workgroups per CU.
-  __shared__ __attribute__((aligned(16))) f32x4 xbuf[kMlaWaves][64];
-  int* const bad_lds = reinterpret_cast<int*>(&xbuf[0][0]);
-
-  // blockIdx.x = (sequence, head group), blockIdx.y = split (XCD balance, as in the
-  // paged decode kernel)
-  const int split = blockIdx.y;
-  const int b = blockIdx.x / p.n_hg;
-  const int hg = blockIdx.x - b * p.n_hg;
-  const int L = min(max(p.lens[b], 0), p.max_len);
-  const int s_begin = split * p.tps;
-  const int s_end = min(s_begin + p.tps, L);
-  if (s_begin >= s_end) return;  // uniform across the workgroup: no barrier reached
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int c16 = lane & 15;
-  const int g4 = lane >> 4;
-  const int hs = wave >> 1;  // head subgroup: MFMA columns = heads 16 hs + c16
-  const int dq = wave & 1;   // output dim half
-  const int head = hg * 32 + hs * 16 + c16;
-  const bool head_live = head < p.Hq;
-
-  int slot0;
-  const int pg0 = mla_page_of(p, s_begin, slot0);
-  int slot1;
-  const int pg1 = mla_page_of(p, s_end - 1, slot1);
-  // invalid page ids staged as -1, read as page 0 and masked (as in the paged decode)
-  bool bad = false;
-  {
-    const int32_t* btrow = p.bt + static_cast<int64_t>(b) * p.bt_stride;
-    for (int i = tid; i <= pg1 - pg0; i += kMlaThreads) {
-      const int phys = btrow[pg0 + i];
-      const bool ok = phys >= 0 && phys < p.num_pages;
-      bt_lds[i] = ok ? phys : -1;
-      bad = bad || !ok;
-    }
-  }
-  const bool wave_bad = __any(bad);  // every lane votes
-  if (lane == 0) bad_lds[wave] = wave_bad ? 1 : 0;
-  // Q^T as the B operand: lane holds head `head`, dims 32 ks + 8 g4 .. +7.
-  u32x4 qreg[KS];
-  {
-    const uint16_t* qr = p.q + b * p.q_sb + static_cast<int64_t>(head_live ? head : 0) * p.q_sh;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(qr + 32 * ks + 8 * g4);
-      qreg[ks] = head_live ? v : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  // Compiler-issued loads (block table, Q) complete before the asm tile loads start.
-  wait_vmcnt0();
-  __syncthreads();
-  const bool any_bad = (bad_lds[0] | bad_lds[1] | bad_lds[2] | bad_lds[3]) != 0;
-
-  const char* pool = reinterpret_cast<const char*>(p.kv);
-  const int n_tiles = (s_end - s_begin + kMlaTile - 1) / kMlaTile;
-  // Load j of this lane fills chunk position (4j + wave) * 64 + lane of a tile: row
-  // pos / CH of the tile, its swizzled 16-byte chunk, from that row's own page.
-  auto issue = [&](int t, int st) {
-    const int t0 = s_begin + t * kMlaTile;
-    uint16_t* dst = ring[st];
-#pragma unroll
-    for (int j = 0; j < LPT; ++j) {
-      const int pos = (4 * j + wave) * 64 + lane;
-      const int row = pos / CH;
-      const int pc = pos - row * CH;
-      const int tok = min(t0 + row, s_end - 1);  // rows past the split are masked
-      int slot;
-      const int pg = mla_page_of(p, tok, slot);
-      const int64_t ro = (static_cast<int64_t>(max(bt_lds[pg - pg0], 0)) * p.P + slot) * DQK * 2;
-      load_lds16_async(pool + ro + (pc ^ mla_swz(row)) * 16, lds_addr(dst + (4 * j + wave) * 512));
-    }
-  };
-
-  // Per-lane operand offsets (elements) inside a tile. K operand of k-step ks, key block
-  // kb: row 16 kb + c16, chunk 4 ks + g4; the swizzle depends on c16 only, so k-steps
-  // two apart differ by 64 elements and key blocks by 16 rows.
-  const int ksw = mla_swz(c16);
-  const int k_rd0 = c16 * DQK + (((0 + g4) ^ ksw) << 3);
-  const int k_rd1 = c16 * DQK + (((4 + g4) ^ ksw) << 3);
-  // V^T operand of dim block db (ds_read_b64_tr_b16 law): this lane supplies key row
-  // 16 kb + 4 g4 + (c16 >> 2) and dims 4 (c16 & 3) .. +3 of the 16-dim block.
-  const int vrow = 4 * g4 + (c16 >> 2);
-  const int vsw = mla_swz(vrow);
-  int v_rd[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int col = dq * DW + 16 * u + 4 * (c16 & 3);
-    v_rd[u] = vrow * DQK + (((col >> 3) ^ vsw) << 3) + (col & 7);
-  }
-
-  f32x4 oacc[DBW];
-#pragma unroll
-  for (int db = 0; db < DBW; ++db) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = kNegInf;
-  float l_run = 0.0f;
-
-  auto compute = [&](int t, const uint16_t* tl) {
-    const int t0 = s_begin + t * kMlaTile;
-    // S^T of the tile's two 16-key blocks: wave (hs, dq) computes block kb = dq for its
-    // head group (even / odd k-steps in two accumulator chains, the K operands read one
-    // k-step ahead) and takes the other block from its partner wave (hs, 1 - dq) through
-    // LDS, so each K byte is read from LDS by two waves instead of four. The exchange
-    // barrier is also what lets the next tile's loads be issued at the top of the
-    // sweep (one barrier fewer per tile). On MI355X -3 % per cfg5 step, bit-identical.
-    auto k_at = [&](int ks, int kb) {
-      return *reinterpret_cast<const u32x4*>(tl + ((ks & 1) ? k_rd1 : k_rd0) + (ks >> 1) * 64 +
-                                             kb * 16 * DQK);
-    };
-    f32x4 sp[2];
-    sp[0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    sp[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    u32x4 a_cur = k_at(0, dq);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u32x4 a_nxt;
-      if (ks + 1 < KS) a_nxt = k_at(ks + 1, dq);
-      __builtin_amdgcn_sched_barrier(0);
-      sp[ks & 1] = E::mfma16(a_cur, qreg[ks], sp[ks & 1]);
-      if (ks + 1 < KS) a_cur = a_nxt;
-    }
-    const f32x4 own = sp[0] + sp[1];
-    xbuf[wave][lane] = own;
-    __syncthreads();  // both blocks of every head group are in xbuf
-    const f32x4 other = xbuf[wave ^ 1][lane];
-    f32x4 sacc[2];
-    sacc[0] = dq == 0 ? own : other;
-    sacc[1] = dq == 0 ? other : own;
-    // S^T lane layout: keys 16 kb + 4 g4 + j of head c16
-    float mt = kNegInf;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tok = t0 + 16 * kb + 4 * g4 + j;
-        bool live = tok < s_end;
-        if (any_bad && live) {
-          int slot;
-          live = bt_lds[mla_page_of(p, tok, slot) - pg0] >= 0;
-        }
-        const float x = live ? sacc[kb][j] * p.score_mul : kNegInf;
-        sacc[kb][j] = x;
-        mt = fmaxf(mt, x);
-      }
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = wave_pair_max(mt);
-    const float m_new = fmaxf(m_run, mt);
-    const bool need = m_new > m_run + kRescaleThresh;
-    if (__any(need)) {
-      const float alpha = need ? fast_exp2(m_run - m_new) : 1.0f;
-      m_run = need ? m_new : m_run;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < DBW; ++db) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) oacc[db][j] *= alpha;
-      }
-    }
-    const float mu = (m_run == kNegInf) ? 0.0f : m_run;
-    u32x2 pk[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      float e[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        e[j] = fast_exp2(sacc[kb][j] - mu);
-        l_run += e[j];
-      }
-      pk[kb] = u32x2{E::pack2(e[0], e[1]), E::pack2(e[2], e[3])};
-    }
-    // One 32-deep MFMA per dim block: k-slots 8 g4 + 0..3 hold keys 4 g4 + 0..3 and
-    // slots 8 g4 + 4..7 keys 16 + 4 g4 + 0..3, in both operands.
-    const u32x4 pb = {pk[0][0], pk[0][1], pk[1][0], pk[1][1]};
-#pragma unroll
-    for (int db = 0; db < DBW; ++db) {
-      const int off = v_rd[db & 3] + (db >> 2) * 64;
-      const u32x2 a0 = lds_read_tr16(tl + off);  // dim 16 db + c16 of keys 4 g4 + 0..3
-      const u32x2 a1 = lds_read_tr16(tl + off + 16 * DQK);  // keys 16 + 4 g4 + 0..3
-      oacc[db] = E::mfma16(u32x4{a0[0], a0[1], a1[0], a1[1]}, pb, oacc[db]);
-    }
-  };
-
-  // Two-stage ring: tile t + 1 is in flight while tile t is computed. The barrier at the
-  // top of iteration t both publishes tile t and shows every wave done with tile t - 1,
-  // whose stage tile t + 1 then refills.
-  static_assert(kMlaStages == 2 && LPT < 64, "two-stage ring, vmcnt range");
-  if (n_tiles > 0) issue(0, 0);
-  for (int t = 0; t < n_tiles; ++t) {
-    wait_vmcnt0();
-    __syncthreads();  // tile t is in LDS; every wave is done with stage (t + 1) & 1
-    if (t + 1 < n_tiles) issue(t + 1, (t + 1) & 1);
-    compute(t, ring[t & 1]);
-  }
-
-  // Partial of this split: O^T lane layout dims 16 db + 4 g4 + j (of this wave's
-  // quarter) for head c16.
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot = wave_pair_sum(l_tot);
-  if (!head_live) return;
-  const int64_t row = (static_cast<int64_t>(b) * p.Hq + head) * p.n_splits + split;
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  // A normalised partial is a convex combination of latent rows, so it fits the
-  // input's 16-bit type: half the partial traffic of fp32 (both the write here and the
-  // combine's read).
-  uint16_t* wo = p.ws_o + row * DV + dq * DW + 4 * g4;
-#pragma unroll
-  for (int db = 0; db < DBW; ++db) {
-    const u32x2 v = {E::pack2(oacc[db][0] * inv, oacc[db][1] * inv),
-                     E::pack2(oacc[db][2] * inv, oacc[db][3] * inv)};
-    *reinterpret_cast<u32x2*>(wo + 16 * db) = v;
-  }
-  if (dq == 0 && g4 == 0) {
-    p.ws_lse[row] = l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : kNegInf;
-  }
-}
-
 // ---------------------------------------------------------------------------------
-// Eight-wave MLA split kernel (latent 512): two waves per SIMD. Wave w takes head
-// subgroup hs = w >> 2 (16 heads as MFMA columns) and output quarter dq = w & 3 (128
-// latent dims). S^T of a 32-token tile is cut into four pieces per head subgroup: key
-// block kb = dq & 1 over k-step half kh = dq >> 1 (9 of the 18 k-steps); each wave
-// computes its piece and the four are summed from LDS as (kh 0 + kh 1) in every wave
-// of the subgroup, so the subgroup's waves hold identical scores and softmax state.
-// Per tile a wave issues 9 S^T MFMAs and 8 P.V MFMAs against 18 and 16 at four waves,
-// with the same LDS operand bytes per workgroup. 84 KiB of LDS (ring, staged block
-// table, 8 KiB of pieces): one workgroup, eight waves, per CU.
+// Eight-wave MLA split kernel (latent DV = 512 or 256): two waves per SIMD. Wave w
+// takes head subgroup hs = w >> 2 (16 heads as MFMA columns) and output quarter
+// dq = w & 3 (DV / 4 latent dims). S^T of a 32-token tile is cut into four pieces per
+// head subgroup: key block kb = dq & 1 over k-step half kh = dq >> 1 (half of the
+// (DV + 64) / 32 k-steps); each wave computes its piece and the four are summed from LDS
+// as (kh 0 + kh 1) in every wave of the subgroup, so the subgroup's waves hold identical
+// scores and softmax state. Against a four-wave layout (two waves per head subgroup,
+// each computing a key block over all k-steps) this issues half the MFMAs per wave with
+// the same LDS operand bytes per workgroup and measured 8-12 % faster except at
+// whole-tile pages (latent 512, unchanged). At latent 512: 84 KiB of LDS (ring, staged
+// block table, 8 KiB of pieces), one workgroup, eight waves, per CU.
 // TILE_PAGE: page_size is a multiple of the 32-token tile, so a tile (they start at
 // multiples of 32) never straddles a page: one wave-uniform page lookup per tile, and
 // each load is the tile's base (SGPRs) plus a per-lane 32-bit offset fixed for the whole
@@ -880,10 +637,9 @@ __global__ __launch_bounds__(kMlaThreads, 2) void mla_decode_split_kernel(const 
 constexpr int kMla8Waves = 8;
 constexpr int kMla8Threads = 64 * kMla8Waves;
 
-template <typename Tag, bool TILE_PAGE>
+template <typename Tag, int DV, bool TILE_PAGE>
 __global__ __launch_bounds__(kMla8Threads, 1) void mla_decode_split8_kernel(const MlaParams p) {
   using E = Elem<Tag>;
-  constexpr int DV = 512;
   constexpr int DQK = DV + kMlaRope;             // 576
   constexpr int CH = DQK / 8;                    // 72 chunks per row
   constexpr int TILE = kMlaTile * DQK;           // elements per tile
@@ -1448,23 +1204,20 @@ namespace {
 template <typename Tag>
 void launch_mla_tag(const MlaParams& mp, const DecodeParams& cp, int dim_v, dim3 grid,
                     hipStream_t s) {
-  // Latent 512 runs the eight-wave kernel: at 32-token-multiple pages it measured the
-  // same as the four-wave one (cfg5, 33.4 against 33.5 us per step), at 16-token pages
-  // (per-row page lookups) 12 % faster (35.8 against 40.6 us). The whole-tile page path
-  // serves latent 512 only: a latent-256 instantiation of it (in the four-wave kernel)
-  // gave wrong scores on MI355X (deterministically, for some lanes of one key block: a
-  // K operand read returned the 16 bytes of a later k-step's read) although its LDS tile
-  // and Q registers were verified correct; latent 256 runs the four-wave kernel with
-  // per-row page lookups.
+  // The whole-tile page path serves latent 512 only: a latent-256 instantiation of it
+  // (in an earlier four-wave kernel) gave wrong scores on MI355X (deterministically, for
+  // some lanes of one key block: a K operand read returned the 16 bytes of a later
+  // k-step's read) although its LDS tile and Q registers were verified correct; latent
+  // 256 uses per-row page lookups at every page size.
   const bool tile_page = mp.P % kMlaTile == 0 && dim_v == 512;
   if (dim_v == 512) {
     if (tile_page) {
-      hipLaunchKernelGGL((mla_decode_split8_kernel<Tag, true>), grid, dim3(kMla8Threads), 0, s, mp);
+      hipLaunchKernelGGL((mla_decode_split8_kernel<Tag, 512, true>), grid, dim3(kMla8Threads), 0, s, mp);
     } else {
-      hipLaunchKernelGGL((mla_decode_split8_kernel<Tag, false>), grid, dim3(kMla8Threads), 0, s, mp);
+      hipLaunchKernelGGL((mla_decode_split8_kernel<Tag, 512, false>), grid, dim3(kMla8Threads), 0, s, mp);
     }
   } else {
-    hipLaunchKernelGGL((mla_decode_split_kernel<Tag, 256>), grid, dim3(kMlaThreads), 0, s, mp);
+    hipLaunchKernelGGL((mla_decode_split8_kernel<Tag, 256, false>), grid, dim3(kMla8Threads), 0, s, mp);
   }
   const unsigned heads4 = static_cast<unsigned>((static_cast<int64_t>(cp.B) * cp.Hq + 3) / 4);
   if (cp.n_splits <= 8) {
