@@ -444,7 +444,7 @@ def bench_mla_decode(steps: int, warmup: int):
         "bytes": nbytes,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS,
-                     "traffic": profiled_traffic("mla_decode_split_kernel_cfg5.md")},
+                     "traffic": profiled_traffic("mla_decode_split8_kernel_cfg5.md")},
         "config": {"workload": "cfg5_mla_decode", "batch": B, "heads_q": H, "latent_dim": lat,
                    "rope_dim": R, "context_len": L, "page_size": P},
     }
