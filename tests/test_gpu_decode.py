@@ -75,6 +75,10 @@ DECODE = [
     ("page_nonpow2", [50, 97], 8, 2, 128, 12, {}, 64),
     ("page4_d64", [3, 40], 2, 2, 64, 4, {}, 32),
     ("g32_colgroups", [70, 300], 32, 1, 128, 16, {}, 64),
+    # a last column group narrower than 16 query heads (20 = 16 + 4, 24 = 16 + 8)
+    ("g20_partial_group", [70, 300, 2049], 40, 2, 128, 16, {}, 64),
+    ("g24_d64_softcap", [40, 513], 24, 1, 64, 16, {"softcap": 20.0}, None),
+    ("g6_d256", [100, 700], 12, 2, 256, 16, {}, 128),
     ("fp16", [100, 400], 8, 2, 128, 16, {"softcap": 50.0}, None),
     ("empty_seq", [0, 50], 4, 2, 64, 16, {}, None),
     ("negative_scale", [50, 300], 8, 2, 128, 16, {"scale": -0.1}, None),
